@@ -1,0 +1,132 @@
+// attn_api.cpp — the extern "C" boundary declared in include/ingot_attn.h.
+//
+// Validates descriptors the way the reference validates forward_batch's arguments
+// (src/metal_backend.mm:421-424, src/cpu_backend.cpp:24-25) but returns error codes instead of
+// throwing, resolves the split-KV partition, carves the caller's workspace, and launches the
+// kernels on the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/ingot_attn.h"
+#include "attn_internal.h"
+
+namespace {
+
+constexpr size_t kCounterBytes = 4096;  // completion counters, one per KV head (<= 1024 heads)
+constexpr size_t kPartFloats = 132;     // per-(split, head) partial record, as in the kernels
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_common(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
+    if (n_head == 0 || n_head_kv == 0 || head_dim == 0) return INGOT_ATTN_EINVAL;
+    if (n_head % n_head_kv != 0) return INGOT_ATTN_EINVAL;
+    if (head_dim != 128) return INGOT_ATTN_EUNSUPPORTED;
+    const uint32_t group = n_head / n_head_kv;
+    if (group < 1 || group > 4) return INGOT_ATTN_EUNSUPPORTED;
+    if (n_head_kv > kCounterBytes / sizeof(unsigned int)) return INGOT_ATTN_EUNSUPPORTED;
+    return INGOT_ATTN_OK;
+}
+
+int check_decode(const IngotAttnDecodeDesc* d) {
+    if (!d) return INGOT_ATTN_EINVAL;
+    const int rc = check_common(d->n_head, d->n_head_kv, d->head_dim);
+    if (rc) return rc;
+    if (d->n_keys == 0 || d->kv_offset % 8 != 0) return INGOT_ATTN_EINVAL;
+    if (!(d->scale > 0.f)) return INGOT_ATTN_EINVAL;
+    return INGOT_ATTN_OK;
+}
+
+int check_prefill(const IngotAttnPrefillDesc* d) {
+    if (!d) return INGOT_ATTN_EINVAL;
+    const int rc = check_common(d->n_head, d->n_head_kv, d->head_dim);
+    if (rc) return rc;
+    if (d->n_tok == 0 || d->kv_offset % 8 != 0) return INGOT_ATTN_EINVAL;
+    if (uint64_t(d->pos) + d->n_tok > 0xffffffffull) return INGOT_ATTN_EINVAL;
+    if (d->q_stride < d->n_head * d->head_dim || d->q_stride % 4 != 0) return INGOT_ATTN_EINVAL;
+    if (!(d->scale > 0.f)) return INGOT_ATTN_EINVAL;
+    return INGOT_ATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
+    if (check_decode(d)) return 0;
+    return ingot::decode_splits(d->n_keys, d->n_head_kv, d->n_splits);
+}
+
+uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
+    if (check_prefill(d)) return 0;
+    return ingot::prefill_splits(d->pos, d->n_tok, d->n_head, d->n_splits);
+}
+
+size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
+    if (check_decode(d)) return 0;
+    const uint32_t splits = ingot::decode_splits(d->n_keys, d->n_head_kv, d->n_splits);
+    return kCounterBytes + size_t(splits) * d->n_head * kPartFloats * sizeof(float);
+}
+
+size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d) {
+    if (check_prefill(d)) return 0;
+    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head, d->n_splits);
+    const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head * kPartFloats * sizeof(float) : 0;
+    return kCounterBytes + parts;
+}
+
+int ingot_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                      void* workspace, size_t workspace_bytes, const IngotAttnDecodeDesc* d,
+                      void* stream) {
+    const int rc = check_decode(d);
+    if (rc) return rc;
+    if (!q || !k_cache || !v_cache || !out || !workspace) return INGOT_ATTN_EINVAL;
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) ||
+        !aligned16(workspace))
+        return INGOT_ATTN_EINVAL;
+    if (workspace_bytes < ingot_attn_decode_workspace_size(d)) return INGOT_ATTN_EWORKSPACE;
+    const uint32_t splits = ingot::decode_splits(d->n_keys, d->n_head_kv, d->n_splits);
+    auto* counters = static_cast<unsigned int*>(workspace);
+    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
+    const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
+    const int lrc = ingot::launch_decode(q, k, v, out, part, counters, d->n_keys, splits,
+                                         d->n_head_kv, d->n_head / d->n_head_kv, d->scale,
+                                         static_cast<hipStream_t>(stream));
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+}
+
+int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
+                       void* workspace, size_t workspace_bytes, const IngotAttnPrefillDesc* d,
+                       void* stream) {
+    const int rc = check_prefill(d);
+    if (rc) return rc;
+    if (!q || !k_cache || !v_cache || !out || !workspace) return INGOT_ATTN_EINVAL;
+    if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out) ||
+        !aligned16(workspace))
+        return INGOT_ATTN_EINVAL;
+    if (workspace_bytes < ingot_attn_prefill_workspace_size(d)) return INGOT_ATTN_EWORKSPACE;
+    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head, d->n_splits);
+    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
+    const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
+    const int lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride,
+                                          d->n_head_kv, d->n_head / d->n_head_kv, splits, d->scale,
+                                          static_cast<hipStream_t>(stream));
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+}
+
+const char* ingot_attn_strerror(int code) {
+    switch (code) {
+        case INGOT_ATTN_OK: return "ok";
+        case INGOT_ATTN_EINVAL: return "invalid argument (null/misaligned pointer, zero size or position out of range)";
+        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (head_dim must be 128, n_head/n_head_kv in 1..4)";
+        case INGOT_ATTN_EWORKSPACE: return "workspace smaller than the *_workspace_size() figure";
+        case INGOT_ATTN_EHIP: return "HIP launch failed";
+        default: return "unknown error";
+    }
+}
+
+const char* ingot_attn_version(void) { return "ingot-attn-gfx950 0.1"; }
+
+}  // extern "C"

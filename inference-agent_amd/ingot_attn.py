@@ -1,0 +1,191 @@
+"""ctypes binding of libingot_attn.so, the C ABI declared in include/ingot_attn.h.
+
+This is the host-side mirror of the attention step of Ingot's `Backend` (src/backend.h:9-23;
+the Metal dispatcher is `encode_attention`, src/metal_backend.mm:336-383). Device memory and
+streams come from PyTorch (plumbing only); every computation runs in the HIP library. There is
+no CPU fallback: if the library is missing or fails, these functions raise, as the reference
+raises std::runtime_error (src/metal_backend.mm:421-424, 462).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from ctypes import c_float, c_int, c_size_t, c_uint32, c_uint64, c_void_p
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libingot_attn.so")
+
+# Exported symbols, as declared in include/ingot_attn.h.
+EXPORTS = (
+    "ingot_attn_decode_workspace_size",
+    "ingot_attn_prefill_workspace_size",
+    "ingot_attn_decode_splits",
+    "ingot_attn_prefill_splits",
+    "ingot_attn_decode",
+    "ingot_attn_prefill",
+    "ingot_attn_strerror",
+    "ingot_attn_version",
+)
+
+
+class DecodeDesc(ctypes.Structure):
+    """IngotAttnDecodeDesc; mirrors AttnDecParams (src/metal_backend.mm:32)."""
+
+    _fields_ = [
+        ("n_head", c_uint32),
+        ("n_head_kv", c_uint32),
+        ("head_dim", c_uint32),
+        ("n_keys", c_uint32),
+        ("kv_offset", c_uint64),
+        ("n_splits", c_uint32),
+        ("scale", c_float),
+    ]
+
+
+class PrefillDesc(ctypes.Structure):
+    """IngotAttnPrefillDesc; mirrors AttnPrefillParams (src/metal_backend.mm:33)."""
+
+    _fields_ = [
+        ("n_head", c_uint32),
+        ("n_head_kv", c_uint32),
+        ("head_dim", c_uint32),
+        ("pos", c_uint32),
+        ("n_tok", c_uint32),
+        ("kv_offset", c_uint64),
+        ("q_stride", c_uint32),
+        ("n_splits", c_uint32),
+        ("scale", c_float),
+    ]
+
+
+_lib = None
+
+
+def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
+    """Loads the HIP library (once). Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"libingot_attn.so not found at {path}: build it first "
+            "(python -c 'import __graft_entry__ as g; g.build()')"
+        )
+    lib = ctypes.CDLL(path)
+    PD, PP = ctypes.POINTER(DecodeDesc), ctypes.POINTER(PrefillDesc)
+    lib.ingot_attn_decode_workspace_size.argtypes = [PD]
+    lib.ingot_attn_decode_workspace_size.restype = c_size_t
+    lib.ingot_attn_prefill_workspace_size.argtypes = [PP]
+    lib.ingot_attn_prefill_workspace_size.restype = c_size_t
+    lib.ingot_attn_decode_splits.argtypes = [PD]
+    lib.ingot_attn_decode_splits.restype = c_uint32
+    lib.ingot_attn_prefill_splits.argtypes = [PP]
+    lib.ingot_attn_prefill_splits.restype = c_uint32
+    lib.ingot_attn_decode.argtypes = [c_void_p] * 5 + [c_size_t, PD, c_void_p]
+    lib.ingot_attn_decode.restype = c_int
+    lib.ingot_attn_prefill.argtypes = [c_void_p] * 5 + [c_size_t, PP, c_void_p]
+    lib.ingot_attn_prefill.restype = c_int
+    lib.ingot_attn_strerror.argtypes = [c_int]
+    lib.ingot_attn_strerror.restype = ctypes.c_char_p
+    lib.ingot_attn_version.argtypes = []
+    lib.ingot_attn_version.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def decode_desc(n_head, n_head_kv, head_dim, n_keys, kv_offset=0, n_splits=0, scale=None):
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    return DecodeDesc(n_head, n_head_kv, head_dim, n_keys, kv_offset, n_splits, scale)
+
+
+def prefill_desc(n_head, n_head_kv, head_dim, pos, n_tok, kv_offset=0, q_stride=None, n_splits=0,
+                 scale=None):
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    q_stride = n_head * head_dim if q_stride is None else q_stride
+    return PrefillDesc(n_head, n_head_kv, head_dim, pos, n_tok, kv_offset, q_stride, n_splits, scale)
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().ingot_attn_strerror(rc).decode()
+        raise RuntimeError(f"{what} failed: {msg} (code {rc})")
+
+
+class Workspace:
+    """A zero-initialised device workspace that grows on demand (never shrinks).
+
+    The library leaves its completion counters at zero after every call, so the buffer is
+    zeroed only when (re)allocated.
+    """
+
+    def __init__(self, device="cuda"):
+        self.device = device
+        self.buf = None
+
+    def get(self, nbytes: int):
+        import torch
+
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=self.device)
+        return self.buf
+
+
+_default_ws = {}
+
+
+def _workspace(device):
+    key = str(device)
+    if key not in _default_ws:
+        _default_ws[key] = Workspace(device)
+    return _default_ws[key]
+
+
+def _stream_ptr(stream):
+    import torch
+
+    s = torch.cuda.current_stream() if stream is None else stream
+    return c_void_p(s.cuda_stream)
+
+
+def attn_decode(q, k_cache, v_cache, out, desc: DecodeDesc, stream=None, workspace=None):
+    """One decode step: out[n_head*hd] = attention of q over cache rows 0..n_keys-1.
+
+    q, out: f32 CUDA tensors; k_cache, v_cache: f16 (or int16/uint16 bit-views) CUDA tensors
+    holding the [layer][n_ctx][n_head_kv*hd] cache. Launches on `stream` (default: torch's
+    current stream) and returns without synchronizing.
+    """
+    lib = load_library()
+    nbytes = lib.ingot_attn_decode_workspace_size(ctypes.byref(desc))
+    if nbytes == 0:
+        _check(-1, "ingot_attn_decode_workspace_size")
+    ws = (workspace or _workspace(q.device)).get(nbytes)
+    rc = lib.ingot_attn_decode(
+        c_void_p(q.data_ptr()), c_void_p(k_cache.data_ptr()), c_void_p(v_cache.data_ptr()),
+        c_void_p(out.data_ptr()), c_void_p(ws.data_ptr()), c_size_t(ws.numel()),
+        ctypes.byref(desc), _stream_ptr(stream))
+    _check(rc, "ingot_attn_decode")
+    return out
+
+
+def attn_prefill(q, k_cache, v_cache, out, desc: PrefillDesc, stream=None, workspace=None):
+    """Causal prefill of desc.n_tok queries at positions desc.pos.. over the cache."""
+    lib = load_library()
+    nbytes = lib.ingot_attn_prefill_workspace_size(ctypes.byref(desc))
+    if nbytes == 0:
+        _check(-1, "ingot_attn_prefill_workspace_size")
+    ws = (workspace or _workspace(q.device)).get(nbytes)
+    rc = lib.ingot_attn_prefill(
+        c_void_p(q.data_ptr()), c_void_p(k_cache.data_ptr()), c_void_p(v_cache.data_ptr()),
+        c_void_p(out.data_ptr()), c_void_p(ws.data_ptr()), c_size_t(ws.numel()),
+        ctypes.byref(desc), _stream_ptr(stream))
+    _check(rc, "ingot_attn_prefill")
+    return out
+
+
+def decode_splits(desc: DecodeDesc) -> int:
+    return int(load_library().ingot_attn_decode_splits(ctypes.byref(desc)))
+
+
+def prefill_splits(desc: PrefillDesc) -> int:
+    return int(load_library().ingot_attn_prefill_splits(ctypes.byref(desc)))

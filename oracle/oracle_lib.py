@@ -1,0 +1,89 @@
+"""ctypes binding of liboracle.so — the CPU restatement of Ingot's attention.
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg, as the checker and the CPU baseline. The product path never imports it.
+Reference lines each function follows are cited in attn_oracle.cpp.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from ctypes import c_float, c_int, c_size_t, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} missing: run `make -C oracle`")
+        L = ctypes.CDLL(LIB_PATH)
+        L.oracle_f32_to_f16.argtypes = [c_void_p, c_void_p, c_size_t]
+        L.oracle_f16_to_f32.argtypes = [c_void_p, c_void_p, c_size_t]
+        L.oracle_softmax.argtypes = [c_void_p, c_size_t]
+        L.oracle_attn_decode.argtypes = [c_void_p] * 4 + [c_int] * 4 + [c_float, c_int]
+        L.oracle_attn_decode.restype = c_int
+        L.oracle_attn_prefill.argtypes = [c_void_p] * 4 + [c_int] * 6 + [c_float, c_int]
+        L.oracle_attn_prefill.restype = c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    return c_void_p(a.ctypes.data)
+
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().oracle_f32_to_f16(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().oracle_f16_to_f32(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def softmax(x: np.ndarray) -> np.ndarray:
+    x = np.array(x, dtype=np.float32, copy=True)
+    lib().oracle_softmax(_ptr(x), x.size)
+    return x
+
+
+def attn_decode(q, k_bits, v_bits, n_head, n_head_kv, head_dim, n_keys, scale=None, threads=1):
+    """q f32 [n_head*hd]; k_bits/v_bits u16 [>= n_keys][n_head_kv*hd] -> out f32 [n_head*hd]."""
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+    k_bits = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    v_bits = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    out = np.empty(n_head * head_dim, dtype=np.float32)
+    rc = lib().oracle_attn_decode(_ptr(q), _ptr(k_bits), _ptr(v_bits), _ptr(out), n_head,
+                                  n_head_kv, head_dim, n_keys, scale, threads)
+    if rc != 0:
+        raise ValueError("oracle_attn_decode: bad arguments")
+    return out
+
+
+def attn_prefill(q, k_bits, v_bits, n_head, n_head_kv, head_dim, pos, n_tok, scale=None,
+                 threads=1):
+    """q f32 [n_tok][n_head*hd]; cache rows 0..pos+n_tok-1 -> out f32 [n_tok][n_head*hd]."""
+    scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
+    q = np.ascontiguousarray(q, dtype=np.float32).reshape(n_tok, -1)
+    k_bits = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    v_bits = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    out = np.zeros_like(q)
+    rc = lib().oracle_attn_prefill(_ptr(q), _ptr(k_bits), _ptr(v_bits), _ptr(out), n_head,
+                                   n_head_kv, head_dim, pos, n_tok, q.shape[1], scale, threads)
+    if rc != 0:
+        raise ValueError("oracle_attn_prefill: bad arguments")
+    return out

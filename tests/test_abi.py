@@ -1,0 +1,117 @@
+"""The C ABI library: it loads without a GPU, exports every symbol include/*.h declares, its
+descriptor structs match the C layout, and its host-side validation behaves as documented.
+No compute call is made here (there is no GPU in the CPU suite)."""
+from __future__ import annotations
+
+import ctypes
+import glob
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+from conftest import PKG, ROOT, ensure_built
+
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def _declared_functions():
+    names = []
+    for path in sorted(glob.glob(os.path.join(INCLUDE, "*.h"))):
+        text = open(path).read()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"^[A-Za-z_][\w\s\*]*?\b(ingot_\w+)\s*\(", text, flags=re.M):
+            names.append(m.group(1))
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    ensure_built("lib")
+    import ingot_attn
+
+    return ingot_attn.load_library()
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    assert "ingot_attn_decode" in names and "ingot_attn_prefill" in names
+    import ingot_attn
+
+    assert sorted(ingot_attn.EXPORTS) == sorted(names)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    so = os.path.join(PKG, "libingot_attn.so")
+    dyn = subprocess.run(["nm", "-D", "--defined-only", so], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in dyn.splitlines() if line.strip()}
+    for name in _declared_functions():
+        assert name in exported, f"{name} declared in include/ but not exported"
+        assert getattr(lib, name) is not None
+
+
+def test_struct_layout_matches_c():
+    import ingot_attn
+
+    src = r"""
+    #include <stdio.h>
+    #include <stddef.h>
+    #include "ingot_attn.h"
+    int main(void) {
+        printf("%zu %zu %zu %zu %zu\n", sizeof(IngotAttnDecodeDesc),
+               offsetof(IngotAttnDecodeDesc, kv_offset), offsetof(IngotAttnDecodeDesc, scale),
+               sizeof(IngotAttnPrefillDesc), offsetof(IngotAttnPrefillDesc, kv_offset));
+        printf("%zu %zu\n", offsetof(IngotAttnPrefillDesc, q_stride),
+               offsetof(IngotAttnPrefillDesc, scale));
+        return 0;
+    }
+    """
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "l.c")
+        exe = os.path.join(d, "l")
+        open(c, "w").write(src)
+        subprocess.run(["gcc", "-I", INCLUDE, c, "-o", exe], check=True)
+        vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True).stdout.split()]
+    D, P = ingot_attn.DecodeDesc, ingot_attn.PrefillDesc
+    assert vals == [ctypes.sizeof(D), D.kv_offset.offset, D.scale.offset, ctypes.sizeof(P),
+                    P.kv_offset.offset, P.q_stride.offset, P.scale.offset]
+
+
+def test_host_validation(lib):
+    import ingot_attn as ia
+
+    ok = ia.decode_desc(24, 8, 128, 4096)
+    assert lib.ingot_attn_decode_workspace_size(ctypes.byref(ok)) > 0
+    assert ia.decode_splits(ok) >= 1
+    for bad in (ia.decode_desc(24, 8, 64, 4096),   # head_dim != 128
+                ia.decode_desc(24, 7, 128, 4096),  # not divisible
+                ia.decode_desc(40, 8, 128, 4096),  # group 5
+                ia.decode_desc(24, 8, 128, 0)):    # no keys
+        assert lib.ingot_attn_decode_workspace_size(ctypes.byref(bad)) == 0
+    # null pointers are rejected before any HIP call
+    rc = lib.ingot_attn_decode(None, None, None, None, None, 0, ctypes.byref(ok), None)
+    assert rc == -1
+    rc = lib.ingot_attn_decode(None, None, None, None, None, 0,
+                               ctypes.byref(ia.decode_desc(24, 8, 64, 10)), None)
+    assert rc == -2
+    p = ia.prefill_desc(24, 8, 128, 3584, 512)
+    assert lib.ingot_attn_prefill_workspace_size(ctypes.byref(p)) > 0
+    assert 1 <= ia.prefill_splits(p) <= 16
+    bad = ia.prefill_desc(24, 8, 128, 0, 512, q_stride=100)
+    assert lib.ingot_attn_prefill_workspace_size(ctypes.byref(bad)) == 0
+    assert lib.ingot_attn_strerror(-3).decode().startswith("workspace")
+    assert lib.ingot_attn_version().decode().startswith("ingot-attn")
+
+
+def test_split_resolution(lib):
+    import ingot_attn as ia
+
+    for n_keys in (1, 2, 63, 64, 65, 511, 512, 4096, 8192, 100000):
+        for req in (0, 1, 3, 64, 5000):
+            s = ia.decode_splits(ia.decode_desc(24, 8, 128, n_keys, n_splits=req))
+            assert 1 <= s <= min(n_keys, 1024)
+            per = -(-n_keys // s)
+            assert (s - 1) * per < n_keys  # no empty split

@@ -1,0 +1,137 @@
+"""GPU parity of the split-KV decode kernel against the CPU oracle, through the C ABI."""
+from __future__ import annotations
+
+import math
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import assert_parity, ensure_built
+
+pytestmark = pytest.mark.gpu
+
+H, HKV, HD = 24, 8, 128
+KV = HKV * HD
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a GPU")
+    ensure_built("lib")
+    import ingot_attn
+
+    ingot_attn.load_library()
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _run_decode(dev, q, kb, vb, n_head, n_head_kv, n_keys, kv_offset=0, n_splits=0):
+    import torch
+    import ingot_attn as ia
+
+    print(f"[decode] n_head={n_head} n_head_kv={n_head_kv} n_keys={n_keys} "
+          f"kv_offset={kv_offset} n_splits={n_splits}", flush=True)
+    qd = _t(q.astype(np.float32), dev)
+    kd = _t(kb.view(np.int16), dev)
+    vd = _t(vb.view(np.int16), dev)
+    out = torch.full((n_head * HD,), float("nan"), dtype=torch.float32, device=dev)
+    desc = ia.decode_desc(n_head, n_head_kv, HD, n_keys, kv_offset=kv_offset, n_splits=n_splits)
+    ia.attn_decode(qd, kd, vd, out, desc)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _inputs(seed, n_head, n_head_kv, L, kv_scale=1.0, n_ctx=None):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    n_ctx = L if n_ctx is None else n_ctx
+    q = rng.standard_normal(n_head * HD).astype(np.float32)
+    kb = np.full((n_ctx, n_head_kv * HD), 0x7E00, dtype=np.uint16)  # NaN past n_keys
+    vb = np.full((n_ctx, n_head_kv * HD), 0x7E00, dtype=np.uint16)
+    kb[:L] = (rng.standard_normal((L, n_head_kv * HD)) * kv_scale).astype(np.float16).view(np.uint16)
+    vb[:L] = (rng.standard_normal((L, n_head_kv * HD)) * kv_scale).astype(np.float16).view(np.uint16)
+    return q, kb, vb
+
+
+@pytest.mark.parametrize("name", ["C1-decode-512", "C3-decode-4096", "C5-decode-1024",
+                                  "C5-decode-2048", "C5-decode-4096", "C5-decode-8192"])
+def test_decode_configs(dev, oracle_mod, name):
+    import workloads as W
+
+    w = W.BY_NAME[name]
+    q, kb, vb = W.make_inputs(w)
+    got = _run_decode(dev, q, kb, vb, H, HKV, w.n_keys)
+    want = oracle_mod.attn_decode(q, kb, vb, H, HKV, HD, w.n_keys, threads=8)
+    m, r = assert_parity(got, want, name)
+    print(f"{name}: max|d|={m:.2e} rel-L2={r:.2e}")
+
+
+@pytest.mark.parametrize("L", [1, 2, 3, 15, 16, 17, 63, 64, 65, 100, 127, 129, 1000, 4097])
+def test_decode_ragged_lengths(dev, oracle_mod, L):
+    q, kb, vb = _inputs(1000 + L, H, HKV, L, n_ctx=L + 40)
+    got = _run_decode(dev, q, kb, vb, H, HKV, L)
+    want = oracle_mod.attn_decode(q, kb, vb, H, HKV, HD, L)
+    assert_parity(got, want, f"L={L}")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 64, 200, 1024])
+def test_decode_split_invariance(dev, oracle_mod, splits):
+    L = 2000
+    q, kb, vb = _inputs(77, H, HKV, L)
+    got = _run_decode(dev, q, kb, vb, H, HKV, L, n_splits=splits)
+    want = oracle_mod.attn_decode(q, kb, vb, H, HKV, HD, L)
+    assert_parity(got, want, f"splits={splits}")
+
+
+@pytest.mark.parametrize("n_head,n_head_kv", [(8, 8), (8, 4), (16, 4), (32, 8), (3, 1)])
+def test_decode_group_sizes(dev, oracle_mod, n_head, n_head_kv):
+    L = 333
+    q, kb, vb = _inputs(5 + n_head, n_head, n_head_kv, L)
+    got = _run_decode(dev, q, kb, vb, n_head, n_head_kv, L)
+    want = oracle_mod.attn_decode(q, kb, vb, n_head, n_head_kv, HD, L)
+    assert_parity(got, want, f"G={n_head // n_head_kv}")
+
+
+def test_decode_layer_offset(dev, oracle_mod):
+    # A 4-layer cache [layer][n_ctx][kv_dim]; layers other than 2 hold NaN, so reading outside
+    # the selected slice shows up as a non-finite output.
+    n_ctx, L, layer = 600, 517, 2
+    q, kb1, vb1 = _inputs(9, H, HKV, L, n_ctx=n_ctx)
+    kb = np.full((4 * n_ctx, KV), 0x7E00, dtype=np.uint16)
+    vb = np.full((4 * n_ctx, KV), 0x7E00, dtype=np.uint16)
+    kb[layer * n_ctx:(layer + 1) * n_ctx] = kb1
+    vb[layer * n_ctx:(layer + 1) * n_ctx] = vb1
+    got = _run_decode(dev, q, kb, vb, H, HKV, L, kv_offset=layer * n_ctx * KV)
+    want = oracle_mod.attn_decode(q, kb1, vb1, H, HKV, HD, L)
+    assert_parity(got, want, "layer offset")
+
+
+def test_decode_repeated_calls_reuse_workspace(dev, oracle_mod):
+    # The completion counters must be back at zero after each call.
+    for i, L in enumerate((4096, 700, 4096, 65)):
+        q, kb, vb = _inputs(300 + i, H, HKV, L)
+        got = _run_decode(dev, q, kb, vb, H, HKV, L)
+        want = oracle_mod.attn_decode(q, kb, vb, H, HKV, HD, L, threads=8)
+        assert_parity(got, want, f"call {i}")
+
+
+def test_decode_closed_forms(dev):
+    # single key -> v0; all K equal -> mean of V; dominant key -> its V row
+    rng = np.random.Generator(np.random.PCG64(11))
+    q = rng.standard_normal(H * HD).astype(np.float32)
+    v = rng.standard_normal((300, KV)).astype(np.float16)
+    k = np.tile(rng.standard_normal((1, KV)).astype(np.float16), (300, 1))
+    got = _run_decode(dev, q, k.view(np.uint16), v.view(np.uint16), H, HKV, 1).reshape(H, HD)
+    v0 = v[0].astype(np.float32).reshape(HKV, HD)
+    np.testing.assert_allclose(got, np.repeat(v0, 3, axis=0), atol=1e-6)
+    got = _run_decode(dev, q, k.view(np.uint16), v.view(np.uint16), H, HKV, 300).reshape(H, HD)
+    mean = v.astype(np.float64).reshape(300, HKV, HD).mean(axis=0)
+    np.testing.assert_allclose(got, np.repeat(mean, 3, axis=0), atol=1e-5)

@@ -1,0 +1,149 @@
+"""GPU parity of the causal MFMA prefill kernel against the CPU oracle, through the C ABI."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_parity, ensure_built
+
+pytestmark = pytest.mark.gpu
+
+H, HKV, HD = 24, 8, 128
+KV = HKV * HD
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a GPU")
+    ensure_built("lib")
+    import ingot_attn
+
+    ingot_attn.load_library()
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _run_prefill(dev, q, kb, vb, n_head, n_head_kv, pos, n_tok, kv_offset=0, n_splits=0,
+                 q_stride=None):
+    import torch
+    import ingot_attn as ia
+
+    q_stride = n_head * HD if q_stride is None else q_stride
+    print(f"[prefill] n_head={n_head} n_head_kv={n_head_kv} pos={pos} n_tok={n_tok} "
+          f"kv_offset={kv_offset} n_splits={n_splits} q_stride={q_stride}", flush=True)
+    qd = _t(q.astype(np.float32), dev)
+    kd = _t(kb.view(np.int16), dev)
+    vd = _t(vb.view(np.int16), dev)
+    out = torch.full(qd.shape, float("nan"), dtype=torch.float32, device=dev)
+    desc = ia.prefill_desc(n_head, n_head_kv, HD, pos, n_tok, kv_offset=kv_offset,
+                           q_stride=q_stride, n_splits=n_splits)
+    ia.attn_prefill(qd, kd, vd, out, desc)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def _inputs(seed, n_head, n_head_kv, pos, n_tok, n_ctx=None):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    L = pos + n_tok
+    n_ctx = L if n_ctx is None else n_ctx
+    q = rng.standard_normal((n_tok, n_head * HD)).astype(np.float32)
+    kb = np.full((n_ctx, n_head_kv * HD), 0x7E00, dtype=np.uint16)
+    vb = np.full((n_ctx, n_head_kv * HD), 0x7E00, dtype=np.uint16)
+    kb[:L] = rng.standard_normal((L, n_head_kv * HD)).astype(np.float16).view(np.uint16)
+    vb[:L] = rng.standard_normal((L, n_head_kv * HD)).astype(np.float16).view(np.uint16)
+    return q, kb, vb
+
+
+@pytest.mark.parametrize("name", ["C2-prefill-512@0", "C4-prefill-512@3584"])
+def test_prefill_configs(dev, oracle_mod, name):
+    import workloads as W
+
+    w = W.BY_NAME[name]
+    q, kb, vb = W.make_inputs(w)
+    got = _run_prefill(dev, q, kb, vb, H, HKV, w.pos, w.n_tok)
+    want = oracle_mod.attn_prefill(q, kb, vb, H, HKV, HD, w.pos, w.n_tok, threads=16)
+    m, r = assert_parity(got, want, name)
+    print(f"{name}: max|d|={m:.2e} rel-L2={r:.2e}")
+
+
+def test_prefill_c5_sampled_rows(dev, oracle_mod):
+    # 2048 queries at 6144 over 8192 keys: the full oracle takes minutes, so a spread of rows
+    # (first, last, tile and split boundaries) is checked against oracle decode steps, each of
+    # which equals the corresponding prefill row (src/backend.h:16-20).
+    import workloads as W
+
+    w = W.C5_PREFILL
+    q, kb, vb = W.make_inputs(w)
+    got = _run_prefill(dev, q, kb, vb, H, HKV, w.pos, w.n_tok)
+    rows = sorted({0, 1, 31, 32, 63, 64, 511, 1000, 1023, 1024, 1535, 2015, 2046, 2047})
+    want = np.stack([oracle_mod.attn_decode(q[i], kb, vb, H, HKV, HD, w.pos + i + 1, threads=8)
+                     for i in rows])
+    assert_parity(got[rows], want, "C5 prefill sampled rows")
+
+
+@pytest.mark.parametrize("pos,n_tok", [(0, 1), (0, 2), (0, 7), (0, 33), (5, 64), (100, 65),
+                                       (63, 1), (64, 31), (1000, 97), (0, 160)])
+def test_prefill_ragged(dev, oracle_mod, pos, n_tok):
+    q, kb, vb = _inputs(pos * 7 + n_tok, H, HKV, pos, n_tok, n_ctx=pos + n_tok + 70)
+    got = _run_prefill(dev, q, kb, vb, H, HKV, pos, n_tok)
+    want = oracle_mod.attn_prefill(q, kb, vb, H, HKV, HD, pos, n_tok, threads=8)
+    assert_parity(got, want, f"pos={pos} n_tok={n_tok}")
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 5, 16])
+def test_prefill_split_invariance(dev, oracle_mod, splits):
+    pos, n_tok = 900, 100
+    q, kb, vb = _inputs(31, H, HKV, pos, n_tok)
+    got = _run_prefill(dev, q, kb, vb, H, HKV, pos, n_tok, n_splits=splits)
+    want = oracle_mod.attn_prefill(q, kb, vb, H, HKV, HD, pos, n_tok, threads=8)
+    assert_parity(got, want, f"splits={splits}")
+
+
+@pytest.mark.parametrize("n_head,n_head_kv", [(8, 8), (8, 4), (16, 4), (3, 1)])
+def test_prefill_group_sizes(dev, oracle_mod, n_head, n_head_kv):
+    pos, n_tok = 70, 90
+    q, kb, vb = _inputs(n_head, n_head, n_head_kv, pos, n_tok)
+    got = _run_prefill(dev, q, kb, vb, n_head, n_head_kv, pos, n_tok)
+    want = oracle_mod.attn_prefill(q, kb, vb, n_head, n_head_kv, HD, pos, n_tok)
+    assert_parity(got, want, f"G={n_head // n_head_kv}")
+
+
+def test_prefill_layer_offset_and_stride(dev, oracle_mod):
+    # layer slice 1 of a 3-layer cache (other layers NaN) and a padded q/out row stride
+    n_ctx, pos, n_tok = 300, 150, 77
+    q, kb1, vb1 = _inputs(42, H, HKV, pos, n_tok, n_ctx=n_ctx)
+    kb = np.full((3 * n_ctx, KV), 0x7E00, dtype=np.uint16)
+    vb = np.full((3 * n_ctx, KV), 0x7E00, dtype=np.uint16)
+    kb[n_ctx:2 * n_ctx] = kb1
+    vb[n_ctx:2 * n_ctx] = vb1
+    stride = H * HD + 64
+    qp = np.zeros((n_tok, stride), dtype=np.float32)
+    qp[:, : H * HD] = q
+    got = _run_prefill(dev, qp, kb, vb, H, HKV, pos, n_tok, kv_offset=n_ctx * KV, q_stride=stride)
+    want = oracle_mod.attn_prefill(q, kb1, vb1, H, HKV, HD, pos, n_tok)
+    assert_parity(got[:, : H * HD], want, "offset+stride")
+    assert np.all(np.isnan(got[:, H * HD:])), "wrote outside the heads' columns"
+
+
+def test_prefill_rows_equal_decode_steps(dev):
+    # Property that holds at any size: prefill row i == decode with n_keys = pos+i+1 (both GPU).
+    import torch
+    import ingot_attn as ia
+
+    pos, n_tok = 2000, 96
+    q, kb, vb = _inputs(55, H, HKV, pos, n_tok)
+    got = _run_prefill(dev, q, kb, vb, H, HKV, pos, n_tok)
+    kd, vd = _t(kb.view(np.int16), dev), _t(vb.view(np.int16), dev)
+    for i in (0, 17, 95):
+        out = torch.empty(H * HD, dtype=torch.float32, device=dev)
+        ia.attn_decode(_t(q[i], dev), kd, vd, out, ia.decode_desc(H, HKV, HD, pos + i + 1))
+        torch.cuda.synchronize()
+        assert_parity(got[i], out.cpu().numpy(), f"row {i}")
