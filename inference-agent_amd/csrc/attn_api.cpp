@@ -13,7 +13,7 @@
 
 namespace {
 
-constexpr size_t kCounterBytes = 4096;  // completion counters, one per KV head (<= 1024 heads)
+using ingot::kCounterBytes;
 constexpr size_t kPartFloats = 132;     // per-(split, head) partial record, as in the kernels
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -24,7 +24,7 @@ int check_common(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
     if (head_dim != 128) return INGOT_ATTN_EUNSUPPORTED;
     const uint32_t group = n_head / n_head_kv;
     if (group < 1 || group > 4) return INGOT_ATTN_EUNSUPPORTED;
-    if (n_head_kv > kCounterBytes / sizeof(unsigned int)) return INGOT_ATTN_EUNSUPPORTED;
+    if (n_head_kv > kCounterBytes / (ingot::kCounterStride * sizeof(unsigned int))) return INGOT_ATTN_EUNSUPPORTED;
     return INGOT_ATTN_OK;
 }
 
