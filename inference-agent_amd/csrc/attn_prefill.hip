@@ -5,27 +5,30 @@
 // steps (src/backend.h:16-20, src/cpu_backend.cpp:51-69) and of the reference's attn_prefill
 // (shaders/kernels.metal:518-633, mask `key <= pos+tok`, line 578), re-designed for CDNA4:
 //
-//   - One workgroup = G waves (one per query head of a GQA group) x NQB query blocks of 32.
-//     Every K/V tile (64 keys) is staged once in LDS and read by all G heads' waves.
-//   - Each wave computes S^T = K Q^T with v_mfma_f32_32x32x16_f16 (A = K rows from LDS,
-//     B = Q^T held in registers), so a lane owns one query column: the row max and row sum of
-//     the online softmax are lane-local plus one exchange with lane^32.
-//   - O^T += V^T P^T with the same MFMA. P^T comes straight out of the S^T accumulator layout
-//     (no shuffle); V is stored transposed in LDS with the key order permuted to match, so the
-//     A operand is one 16-byte LDS read.
-//   - Q is pre-scaled by scale*log2(e) and rounded to f16 (the reference rounds Q*scale to
-//     half, shaders/kernels.metal:543); P is rounded to f16 for the PV product (line 588);
-//     S, O, m and l stay f32.
-//   - Causal tile skipping: a wave stops at the last key its last query may see; tiles that
-//     straddle the diagonal are masked per element.
-//   - Split-KV: with n_splits > 1 each workgroup covers a slice of its key tiles and writes
-//     (o, m, l) partials; attn_prefill_combine merges them (log-sum-exp rule of attn_combine,
+//   - A workgroup = NW waves over one KV head; wave w owns 16 queries and ALL G query heads of
+//     the group (48 score columns for G = 3). Every K/V operand read from LDS feeds G MFMAs
+//     (v_mfma_f32_16x16x32_f16), so the GQA sharing happens at register level, on top of the
+//     workgroup-level sharing of each LDS tile.
+//   - K/V tiles (64 keys) are copied HBM -> LDS with global_load_lds (no VGPRs, no VALU) into a
+//     double buffer: the next tile streams in while the current one is computed. 16-byte
+//     chunks are XOR-swizzled per row so that every LDS read below is bank-conflict free.
+//   - S^T = K Q^T: the A operand is a 16-byte LDS read of a K row, B is Q^T held in registers
+//     (pre-scaled by scale*log2(e) and rounded to f16, as the reference rounds Q*scale to half,
+//     shaders/kernels.metal:543). A lane owns one query column, so the online-softmax max/sum
+//     are lane-local plus two exchanges.
+//   - O^T += V^T P^T: P^T comes straight out of the S^T accumulator (rounded to f16, as at
+//     shaders/kernels.metal:588); V^T is read with ds_read_b64_tr_b16 (transposing LDS read),
+//     whose 4-consecutive-key runs match the accumulator's key order, so nothing is shuffled.
+//   - Causal tile skipping per wave; tiles straddling the diagonal are masked per element.
+//   - Split-KV for short chunks (few waves): each split writes (o, m, l) partials and
+//     attn_prefill_combine merges them (log-sum-exp rule of attn_combine,
 //     shaders/kernels.metal:501-516).
 //
-// MFMA 32x32x16 f16 register layouts (wave64, lane l, i = l%32, hb = l/32):
-//   A (32 x 16): lane holds A[i][8*hb + e], e = 0..7
-//   B (16 x 32): lane holds B[8*hb + e][i]
-//   D (32 x 32): lane holds D[8*(r/4) + 4*hb + r%4][i], r = 0..15
+// MFMA 16x16x32 f16 register layouts (wave64, lane l, i = l%16, g = l/16):
+//   A (16 x 32): lane holds A[i][8g + e];  B (32 x 16): lane holds B[8g + e][i];
+//   D (16 x 16): lane holds D[4g + j][i], j = 0..3.
+// ds_read_b64_tr_b16 (per 16-lane group; lane r supplies an address, lane i receives 4 halves):
+//   out[i][j] = halves[4j + i/4][i%4], where halves[r][0..3] are the 4 halves at lane r's address.
 #include "attn_common.h"
 #include "attn_internal.h"
 
@@ -33,188 +36,220 @@ namespace ingot {
 
 namespace {
 
-constexpr int kBN = 64;            // keys per tile
-constexpr int kKS = kHeadDim + 8;  // LDS row stride of K (halves): 272 B
-constexpr int kVS = kBN + 8;       // LDS row stride of V^T (halves): 144 B
+typedef __attribute__((address_space(3))) void lds_void;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __fp16 fp16x4 __attribute__((__vector_size__(8)));  // operand type of ds_read_tr16_b64
+typedef __attribute__((address_space(3))) fp16x4 lds_fp16x4;
+typedef __attribute__((address_space(3))) half8 lds_half8;
 
-// Position of key j (0..15 inside a 16-key group) in a V^T row: swap bits 2 and 3, so that the
-// 8 keys a lane feeds to one PV MFMA ({0-3, 8-11} or {4-7, 12-15}) are contiguous.
-__device__ __forceinline__ int vt_pos(int j) {
-    return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1);
-}
+constexpr int kBN = 64;                        // keys per tile
+constexpr int kRowBytes = kHeadDim * 2;        // 256 B per K/V row in LDS (no padding)
+constexpr int kTileBytes = kBN * kRowBytes;    // 16 KB per K or V tile
+constexpr int kStageBytes = 2 * kTileBytes;    // K + V
 
-__device__ __forceinline__ uint32_t pack_halves(_Float16 lo, _Float16 hi) {
-    const uint32_t a = __builtin_bit_cast(uint16_t, lo), b = __builtin_bit_cast(uint16_t, hi);
-    return a | (b << 16);
-}
+// XOR swizzles of the 16-byte chunk index (0..15) inside a 256-byte row.
+__device__ __forceinline__ int swz_k(int row) { return row & 15; }       // A-operand row reads
+__device__ __forceinline__ int swz_v(int row) { return (row & 7) << 1; }  // transposing reads
 
-template <int G, int NQB>
-__global__ __launch_bounds__(64 * G * NQB) void attn_prefill_kernel(
-    const float* __restrict__ q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
-    float* __restrict__ out, float* __restrict__ part, uint32_t pos, uint32_t n_tok,
-    uint32_t q_stride, uint32_t n_head_kv, uint32_t n_splits, float qscale) {
-    constexpr int NT = 64 * G * NQB;
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[kBN * kKS];
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[kHeadDim * kVS];
+template <int G, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(G == 4 ? 1 : 2)))
+void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict__ K,
+                         const _Float16* __restrict__ V, float* __restrict__ out,
+                         float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
+                         uint32_t n_head_kv, uint32_t n_splits, float qscale) {
+    extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int hh = wave % G, qsb = wave / G;
-    const int li = lane & 31, hb = lane >> 5;
+    const int li = lane & 15, g = lane >> 4;
     const uint32_t kvh = blockIdx.y, split = blockIdx.z;
-    const uint32_t h = kvh * G + hh;
     const size_t kv_dim = size_t(n_head_kv) * kHeadDim;
-    const uint32_t qblk0 = blockIdx.x * 32 * NQB;
-    const uint32_t q0 = qblk0 + qsb * 32;
+    const uint32_t qblk0 = blockIdx.x * 16 * NW;
+    const uint32_t q0 = qblk0 + 16 * wave;
 
     // Keys [0, kend) are visible to some query of this workgroup.
-    const uint32_t qlast_wg = min(n_tok, qblk0 + 32 * NQB) - 1;
+    const uint32_t qlast_wg = min(n_tok, qblk0 + 16 * NW) - 1;
     const uint32_t kend = pos + qlast_wg + 1;
     const uint32_t ntiles = (kend + kBN - 1) / kBN;
     const uint32_t t_begin = uint32_t((uint64_t(split) * ntiles) / n_splits);
     const uint32_t t_end = uint32_t((uint64_t(split + 1) * ntiles) / n_splits);
     // Keys [0, kend_w) are visible to some query of this wave; 0 if the wave has no queries.
-    const uint32_t kend_w = q0 < n_tok ? pos + min(n_tok, q0 + 32) : 0;
+    const uint32_t kend_w = q0 < n_tok ? pos + min(n_tok, q0 + 16) : 0;
     const uint32_t qpos = pos + q0 + li;  // this lane's query position
 
     const _Float16* Kg = K + size_t(kvh) * kHeadDim;
     const _Float16* Vg = V + size_t(kvh) * kHeadDim;
 
-    // B operand Q^T: lane holds Q[q0 + li][16*ks + 8*hb + e] * scale*log2(e), as f16.
-    half8 qb[8];
-    {
-        const uint32_t row = q0 + li;
+    // Tile copy HBM -> LDS: 32 instructions of 1 KB (4 rows) per tile, spread over the waves.
+    // Lane l of an instruction fills physical chunk l%16 of row 4*i + l/16, so it fetches the
+    // logical chunk (l%16) ^ swizzle(row). Rows past kend are clamped to the last visible row
+    // (finite data; those keys are masked, so their P is exactly 0).
+    auto issue_tile = [&](uint32_t t, int buf) {
+        const uint32_t kb = t * kBN;
+        char* stage = smem + buf * kStageBytes;
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            if (row < n_tok) {
+        for (int i = wave; i < 32; i += NW) {
+            const int isv = i >> 4;
+            const int row = 4 * (i & 15) + (lane >> 4);
+            const int phys = lane & 15;
+            const int logical = phys ^ (isv ? swz_v(row) : swz_k(row));
+            const uint32_t key = min(kb + row, kend - 1);
+            const _Float16* src = (isv ? Vg : Kg) + size_t(key) * kv_dim + 8 * logical;
+            char* dst = stage + isv * kTileBytes + (4 * (i & 15)) * kRowBytes;
+            __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
+        }
+    };
+
+    // B operand Q^T per head: lane holds Q[q0 + li][32*ks + 8*g + e] * scale*log2(e), as f16.
+    half8 qb[G][4];
+    {
+        const uint32_t row = min(q0 + li, n_tok - 1);
+#pragma unroll
+        for (int h = 0; h < G; h++)
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
                 const float4v* src = reinterpret_cast<const float4v*>(
-                    q + size_t(row) * q_stride + size_t(h) * kHeadDim + 16 * ks + 8 * hb);
+                    q + size_t(row) * q_stride + (size_t(kvh) * G + h) * kHeadDim + 32 * ks + 8 * g);
                 const float4v a = src[0], b = src[1];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    qb[ks][e] = _Float16(a[e] * qscale);
-                    qb[ks][4 + e] = _Float16(b[e] * qscale);
+                    qb[h][ks][e] = _Float16(a[e] * qscale);
+                    qb[h][ks][4 + e] = _Float16(b[e] * qscale);
                 }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) qb[ks][e] = _Float16(0.f);
             }
-        }
     }
 
-    float16v O[4];
+    float4v O[G][8];
+    float m[G], l[G];
 #pragma unroll
-    for (int d = 0; d < 4; d++) O[d] = float16v{};
-    float m = kNoMax, l = 0.f;
+    for (int h = 0; h < G; h++) {
+        m[h] = kNoMax;
+        l[h] = 0.f;
+#pragma unroll
+        for (int d = 0; d < 8; d++) O[h][d] = float4v{0.f, 0.f, 0.f, 0.f};
+    }
 
-    for (uint32_t t = t_begin; t < t_end; t++) {
+    auto compute_tile = [&](uint32_t t, int buf) {
         const uint32_t kb = t * kBN;
-        __syncthreads();  // the previous tile has been consumed
-        // K tile: Ks[key][dim], 16 chunks of 16 B per key; rows past kend are zero.
-        for (int i = tid; i < kBN * 16; i += NT) {
-            const int key = i >> 4, ch = i & 15;
-            const uint32_t kk = kb + key;
-            half8 val = {};
-            if (kk < kend) val = load_half8(Kg + size_t(kk) * kv_dim + 8 * ch);
-            *reinterpret_cast<half8*>(&Ks[key * kKS + 8 * ch]) = val;
-        }
-        // V tile, transposed: Vt[dim][vt_pos(key)], two keys packed per 32-bit LDS write.
-        for (int i = tid; i < (kBN / 2) * 16; i += NT) {
-            const int pr = i >> 4, ch = i & 15;
-            const uint32_t ka = kb + 2 * pr;
-            half8 va = {}, vb = {};
-            if (ka < kend) va = load_half8(Vg + size_t(ka) * kv_dim + 8 * ch);
-            if (ka + 1 < kend) vb = load_half8(Vg + size_t(ka + 1) * kv_dim + 8 * ch);
-            const int j = (2 * pr) & 15;
-            const int col = ((2 * pr) & ~15) + vt_pos(j);
-#pragma unroll
-            for (int e = 0; e < 8; e++)
-                *reinterpret_cast<uint32_t*>(&Vt[(8 * ch + e) * kVS + col]) = pack_halves(va[e], vb[e]);
-        }
-        __syncthreads();
-        if (kb >= kend_w) continue;  // every key of this tile is in this wave's future
+        if (kb >= kend_w) return;  // every key of this tile is in this wave's future
+        const char* Ks = smem + buf * kStageBytes;
+        const char* Vs = Ks + kTileBytes;
 
-        // S^T (64 keys x 32 queries) as two 32x32 tiles.
-        float16v S[2];
+        // S^T: 4 key tiles of 16 x (G heads x 16 queries).
+        float4v S[4][G];
 #pragma unroll
-        for (int T = 0; T < 2; T++) {
-            S[T] = float16v{};
+        for (int T = 0; T < 4; T++) {
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                const half8 a = *reinterpret_cast<const half8*>(&Ks[(32 * T + li) * kKS + 16 * ks + 8 * hb]);
-                S[T] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[ks], S[T], 0, 0, 0);
+            for (int h = 0; h < G; h++) S[T][h] = float4v{0.f, 0.f, 0.f, 0.f};
+            const int row = 16 * T + li;
+#pragma unroll
+            for (int ks = 0; ks < 4; ks++) {
+                const int chunk = (4 * ks + g) ^ swz_k(row);
+                const half8 a = *reinterpret_cast<const lds_half8*>((const lds_void*)(Ks + row * kRowBytes + 16 * chunk));
+#pragma unroll
+                for (int h = 0; h < G; h++)
+                    S[T][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[h][ks], S[T][h], 0, 0, 0);
             }
         }
         // Causal mask where the tile reaches past the wave's first query position.
         if (kb + kBN - 1 > pos + q0) {
 #pragma unroll
-            for (int T = 0; T < 2; T++)
+            for (int T = 0; T < 4; T++)
 #pragma unroll
-                for (int rr = 0; rr < 16; rr++) {
-                    const uint32_t key = kb + 32 * T + 8 * (rr >> 2) + 4 * hb + (rr & 3);
-                    if (key > qpos) S[T][rr] = -__builtin_inff();
+                for (int j = 0; j < 4; j++) {
+                    const uint32_t key = kb + 16 * T + 4 * g + j;
+                    if (key > qpos) {
+#pragma unroll
+                        for (int h = 0; h < G; h++) S[T][h][j] = -__builtin_inff();
+                    }
                 }
         }
-        float mx = S[0][0];
+        // Online softmax per head (base 2). P^T B operands: step s covers key tiles 2s, 2s+1.
+        half8 P[G][2];
 #pragma unroll
-        for (int T = 0; T < 2; T++)
+        for (int h = 0; h < G; h++) {
+            float mx = S[0][h][0];
 #pragma unroll
-            for (int rr = 0; rr < 16; rr++) mx = fmaxf(mx, S[T][rr]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m, mx);
-        const float alpha = fast_exp2(m - m_new);
-        m = m_new;
-
-        half8 P[4];
-        float ls = 0.f;
+            for (int T = 0; T < 4; T++)
 #pragma unroll
-        for (int T = 0; T < 2; T++)
+                for (int j = 0; j < 4; j++) mx = fmaxf(mx, S[T][h][j]);
+            mx = fmaxf(mx, __shfl_xor(mx, 16));
+            mx = fmaxf(mx, __shfl_xor(mx, 32));
+            const float m_new = fmaxf(m[h], mx);
+            const float alpha = fast_exp2(m[h] - m_new);
+            m[h] = m_new;
+            float ls = 0.f;
 #pragma unroll
-            for (int rr = 0; rr < 16; rr++) {
-                const float p = fast_exp2(S[T][rr] - m_new);
-                ls += p;
-                P[2 * T + (rr >> 3)][rr & 7] = _Float16(p);
+            for (int T = 0; T < 4; T++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float p = fast_exp2(S[T][h][j] - m_new);
+                    ls += p;
+                    P[h][T >> 1][4 * (T & 1) + j] = _Float16(p);
+                }
+            l[h] = l[h] * alpha + ls;
+#pragma unroll
+            for (int d = 0; d < 8; d++) O[h][d] *= alpha;
+        }
+        // O^T (128 dims x (G x 16 queries)) += V^T (128 x 64) P^T (64 x 16) per head.
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+#pragma unroll
+            for (int d = 0; d < 8; d++) {
+                half4 part_[2];
+#pragma unroll
+                for (int half_ = 0; half_ < 2; half_++) {
+                    // this 16-lane group reads keys key0..key0+3 x dims 16d..16d+15
+                    const int key0 = 32 * s + 16 * half_ + 4 * g;
+                    const int row = key0 + (li >> 2);
+                    const int byte = 32 * d + 8 * (li & 3);
+                    const int chunk = (byte >> 4) ^ swz_v(row);
+                    lds_fp16x4* src = (lds_fp16x4*)(lds_void*)const_cast<char*>(Vs + row * kRowBytes + 16 * chunk + (byte & 15));
+                    part_[half_] = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(src));
+                }
+                const half8 a = __builtin_shufflevector(part_[0], part_[1], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+                for (int h = 0; h < G; h++)
+                    O[h][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, P[h][s], O[h][d], 0, 0, 0);
             }
-        l = l * alpha + ls;
-#pragma unroll
-        for (int d = 0; d < 4; d++) O[d] *= alpha;
+        }
+    };
 
-        // O^T (128 dims x 32 queries) += V^T (128 x 64) P^T (64 x 32).
-#pragma unroll
-        for (int d = 0; d < 4; d++)
-#pragma unroll
-            for (int k4 = 0; k4 < 4; k4++) {
-                const half8 a = *reinterpret_cast<const half8*>(&Vt[(32 * d + li) * kVS + 16 * k4 + 8 * hb]);
-                O[d] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, P[k4], O[d], 0, 0, 0);
-            }
+    if (t_begin < t_end) {
+        issue_tile(t_begin, 0);
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        int buf = 0;
+        for (uint32_t t = t_begin; t < t_end; t++) {
+            if (t + 1 < t_end) issue_tile(t + 1, buf ^ 1);
+            compute_tile(t, buf);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile t+1 have landed
+            __syncthreads();                // ... and everyone's; tile t is no longer read
+            buf ^= 1;
+        }
     }
 
-    // Both half-waves hold partial sums of the same rows (same m): add them.
-    l += __shfl_xor(l, 32);
+    // Row sums: the 4 lane groups g hold partial sums of the same query (same m).
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        l[h] += __shfl_xor(l[h], 16);
+        l[h] += __shfl_xor(l[h], 32);
+    }
     const uint32_t row = q0 + li;
     if (row >= n_tok) return;
-    if (n_splits == 1) {
-        const float inv = l > 0.f ? 1.f / l : 0.f;
-        float* dst = out + size_t(row) * q_stride + size_t(h) * kHeadDim;
 #pragma unroll
-        for (int d = 0; d < 4; d++)
+    for (int h = 0; h < G; h++) {
+        const uint32_t head = kvh * G + h;
+        if (n_splits == 1) {
+            const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
+            float* dst = out + size_t(row) * q_stride + size_t(head) * kHeadDim + 4 * g;
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                float4v v = {O[d][4 * g], O[d][4 * g + 1], O[d][4 * g + 2], O[d][4 * g + 3]};
-                *reinterpret_cast<float4v*>(dst + 32 * d + 8 * g + 4 * hb) = v * inv;
-            }
-    } else {
-        const uint32_t n_head = n_head_kv * G;
-        float* dst = part + ((size_t(split) * n_tok + row) * n_head + h) * kPartStride;
+            for (int d = 0; d < 8; d++) *reinterpret_cast<float4v*>(dst + 16 * d) = O[h][d] * inv;
+        } else {
+            const uint32_t n_head = n_head_kv * G;
+            float* dst = part + ((size_t(split) * n_tok + row) * n_head + head) * kPartStride;
 #pragma unroll
-        for (int d = 0; d < 4; d++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                float4v v = {O[d][4 * g], O[d][4 * g + 1], O[d][4 * g + 2], O[d][4 * g + 3]};
-                *reinterpret_cast<float4v*>(dst + 32 * d + 8 * g + 4 * hb) = v;
-            }
-        if (hb == 0) {
-            dst[128] = m;
-            dst[129] = l;
+            for (int d = 0; d < 8; d++) *reinterpret_cast<float4v*>(dst + 16 * d + 4 * g) = O[h][d];
+            if (g == 0) *reinterpret_cast<float4v*>(dst + 128) = float4v{m[h], l[h], 0.f, 0.f};
         }
     }
 }
@@ -245,13 +280,15 @@ __global__ __launch_bounds__(64) void attn_prefill_combine(const float* __restri
     dst[1] = O1 * inv;
 }
 
+constexpr int kNW = 2;  // waves per workgroup (16 queries each)
+
 template <int G>
 int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                      uint32_t n_splits, float qscale, hipStream_t stream) {
-    constexpr int NQB = 1;
-    const dim3 grid((n_tok + 32 * NQB - 1) / (32 * NQB), n_head_kv, n_splits);
-    hipLaunchKernelGGL((attn_prefill_kernel<G, NQB>), grid, dim3(64 * G * NQB), 0, stream, q, k, v,
+    const dim3 grid((n_tok + 16 * kNW - 1) / (16 * kNW), n_head_kv, n_splits);
+    const size_t lds = 2 * kStageBytes;
+    hipLaunchKernelGGL((attn_prefill_kernel<G, kNW>), grid, dim3(64 * kNW), lds, stream, q, k, v,
                        out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale);
     if (hipGetLastError() != hipSuccess) return -4;
     if (n_splits > 1) {
@@ -269,10 +306,10 @@ uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head, uint32_t 
     const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
     uint32_t splits = requested;
     if (splits == 0) {
-        // Aim for >= 2048 waves (2 per SIMD on 256 CUs), keeping >= 2 key tiles per split.
-        const uint32_t waves = ((n_tok + 31) / 32) * n_head;
+        // Aim for >= 2048 waves (2 per SIMD on 256 CUs), keeping >= 4 key tiles per split.
+        const uint32_t waves = ((n_tok + 15) / 16) * max(1u, n_head / 3);
         splits = (2048 + waves - 1) / waves;
-        splits = min(splits, max(1u, max_tiles / 2));
+        splits = min(splits, max(1u, max_tiles / 4));
     }
     return max(1u, min(splits, min(max_tiles, kMaxPrefillSplits)));
 }
