@@ -43,6 +43,7 @@ typedef __attribute__((address_space(3))) fp16x4 lds_fp16x4;
 typedef __attribute__((address_space(3))) half8 lds_half8;
 
 constexpr int kBN = 64;                        // keys per tile
+constexpr float kLazy = 8.f;                   // base-2 headroom before the reference max moves
 constexpr int kRowBytes = kHeadDim * 2;        // 256 B per K/V row in LDS (no padding)
 constexpr int kTileBytes = kBN * kRowBytes;    // 16 KB per K or V tile
 constexpr int kStageBytes = 2 * kTileBytes;    // K + V
@@ -118,12 +119,19 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             }
     }
 
+    // Online-softmax state per head: reference max m (base 2), lane-partial row sum l, O^T.
+    // Scores are produced already shifted (S' = s - m: the MFMA accumulator starts at -m), and
+    // m only moves when some score exceeds it by more than kLazy (or for the first visible
+    // keys), so P = 2^S' <= 2^kLazy and the O rescale is rare. O/l does not depend on the
+    // reference, so this is exact.
     float4v O[G][8];
     float m[G], l[G];
+    bool started[G];
 #pragma unroll
     for (int h = 0; h < G; h++) {
-        m[h] = kNoMax;
+        m[h] = 0.f;
         l[h] = 0.f;
+        started[h] = false;
 #pragma unroll
         for (int d = 0; d < 8; d++) O[h][d] = float4v{0.f, 0.f, 0.f, 0.f};
     }
@@ -134,72 +142,92 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         const char* Ks = smem + buf * kStageBytes;
         const char* Vs = Ks + kTileBytes;
 
-        // S^T: 4 key tiles of 16 x (G heads x 16 queries).
-        float4v S[4][G];
+        // Two halves of 32 keys: scores, online-softmax update, then P*V for each half, so only
+        // 32 keys' worth of S and P is live at a time.
 #pragma unroll
-        for (int T = 0; T < 4; T++) {
+        for (int hs = 0; hs < 2; hs++) {
+            const uint32_t kh = kb + 32 * hs;
+            if (kh >= kend_w) break;
+            // S'^T = K Q^T - m: 2 key tiles of 16 x (G heads x 16 queries).
+            float4v S[2][G];
 #pragma unroll
-            for (int h = 0; h < G; h++) S[T][h] = float4v{0.f, 0.f, 0.f, 0.f};
-            const int row = 16 * T + li;
+            for (int T = 0; T < 2; T++) {
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                const int chunk = (4 * ks + g) ^ swz_k(row);
-                const half8 a = *reinterpret_cast<const lds_half8*>((const lds_void*)(Ks + row * kRowBytes + 16 * chunk));
+                for (int h = 0; h < G; h++) S[T][h] = float4v{-m[h], -m[h], -m[h], -m[h]};
+                const int row = 32 * hs + 16 * T + li;
 #pragma unroll
-                for (int h = 0; h < G; h++)
-                    S[T][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[h][ks], S[T][h], 0, 0, 0);
+                for (int ks = 0; ks < 4; ks++) {
+                    const int chunk = (4 * ks + g) ^ swz_k(row);
+                    const half8 a = *reinterpret_cast<const lds_half8*>((const lds_void*)(Ks + row * kRowBytes + 16 * chunk));
+#pragma unroll
+                    for (int h = 0; h < G; h++)
+                        S[T][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[h][ks], S[T][h], 0, 0, 0);
+                }
             }
-        }
-        // Causal mask where the tile reaches past the wave's first query position.
-        if (kb + kBN - 1 > pos + q0) {
+            // Causal mask where these keys reach past the wave's first query position.
+            if (kh + 31 > pos + q0) {
 #pragma unroll
-            for (int T = 0; T < 4; T++)
+                for (int T = 0; T < 2; T++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const uint32_t key = kb + 16 * T + 4 * g + j;
-                    if (key > qpos) {
+                    for (int j = 0; j < 4; j++) {
+                        const uint32_t key = kh + 16 * T + 4 * g + j;
+                        if (key > qpos) {
 #pragma unroll
-                        for (int h = 0; h < G; h++) S[T][h][j] = -__builtin_inff();
+                            for (int h = 0; h < G; h++) S[T][h][j] = -__builtin_inff();
+                        }
                     }
+            }
+            // Per head: does the reference max have to move? (max over the 4 lanes of a query)
+            float mx[G];
+            bool grow_any = false;
+#pragma unroll
+            for (int h = 0; h < G; h++) {
+                float x = fmaxf(fmaxf(fmaxf(S[0][h][0], S[0][h][1]), fmaxf(S[0][h][2], S[0][h][3])),
+                                fmaxf(fmaxf(S[1][h][0], S[1][h][1]), fmaxf(S[1][h][2], S[1][h][3])));
+                x = fmaxf(x, __shfl_xor(x, 16));
+                x = fmaxf(x, __shfl_xor(x, 32));
+                mx[h] = x;
+                grow_any |= started[h] ? (x > kLazy) : (x > -__builtin_inff());
+            }
+            if (__builtin_amdgcn_ballot_w64(grow_any)) {  // wave-uniform, rare after warm-up
+#pragma unroll
+                for (int h = 0; h < G; h++) {
+                    const bool grow = started[h] ? (mx[h] > kLazy) : (mx[h] > -__builtin_inff());
+                    const float delta = grow ? mx[h] : 0.f;
+                    const float alpha = fast_exp2(-delta);
+                    m[h] += delta;
+                    l[h] *= alpha;
+                    started[h] |= grow;
+#pragma unroll
+                    for (int T = 0; T < 2; T++) S[T][h] -= delta;
+#pragma unroll
+                    for (int d = 0; d < 8; d++) O[h][d] *= alpha;
                 }
-        }
-        // Online softmax per head (base 2). P^T B operands: step s covers key tiles 2s, 2s+1.
-        half8 P[G][2];
+            }
+            // P = 2^S' in f16 (P^T B operand: element 4T + j is key kh+16T+4g+j); row sums from
+            // the same f16 values with v_dot2_f32_f16.
+            half8 P[G];
 #pragma unroll
-        for (int h = 0; h < G; h++) {
-            float mx = S[0][h][0];
+            for (int h = 0; h < G; h++) {
 #pragma unroll
-            for (int T = 0; T < 4; T++)
+                for (int T = 0; T < 2; T++)
 #pragma unroll
-                for (int j = 0; j < 4; j++) mx = fmaxf(mx, S[T][h][j]);
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m[h], mx);
-            const float alpha = fast_exp2(m[h] - m_new);
-            m[h] = m_new;
-            float ls = 0.f;
+                    for (int j = 0; j < 4; j++) P[h][4 * T + j] = _Float16(fast_exp2(S[T][h][j]));
+                const half2v one = {_Float16(1.f), _Float16(1.f)};
+                float ls = l[h];
 #pragma unroll
-            for (int T = 0; T < 4; T++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float p = fast_exp2(S[T][h][j] - m_new);
-                    ls += p;
-                    P[h][T >> 1][4 * (T & 1) + j] = _Float16(p);
-                }
-            l[h] = l[h] * alpha + ls;
-#pragma unroll
-            for (int d = 0; d < 8; d++) O[h][d] *= alpha;
-        }
-        // O^T (128 dims x (G x 16 queries)) += V^T (128 x 64) P^T (64 x 16) per head.
-#pragma unroll
-        for (int s = 0; s < 2; s++) {
+                for (int e = 0; e < 4; e++)
+                    ls = __builtin_amdgcn_fdot2(half2v{P[h][2 * e], P[h][2 * e + 1]}, one, ls, false);
+                l[h] = ls;
+            }
+            // O^T (128 dims x (G x 16 queries)) += V^T (128 x 32) P^T (32 x 16) per head.
 #pragma unroll
             for (int d = 0; d < 8; d++) {
                 half4 part_[2];
 #pragma unroll
                 for (int half_ = 0; half_ < 2; half_++) {
                     // this 16-lane group reads keys key0..key0+3 x dims 16d..16d+15
-                    const int key0 = 32 * s + 16 * half_ + 4 * g;
+                    const int key0 = 32 * hs + 16 * half_ + 4 * g;
                     const int row = key0 + (li >> 2);
                     const int byte = 32 * d + 8 * (li & 3);
                     const int chunk = (byte >> 4) ^ swz_v(row);
@@ -209,7 +237,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                 const half8 a = __builtin_shufflevector(part_[0], part_[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int h = 0; h < G; h++)
-                    O[h][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, P[h][s], O[h][d], 0, 0, 0);
+                    O[h][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, P[h], O[h][d], 0, 0, 0);
             }
         }
     };
@@ -249,7 +277,8 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             float* dst = part + ((size_t(split) * n_tok + row) * n_head + head) * kPartStride;
 #pragma unroll
             for (int d = 0; d < 8; d++) *reinterpret_cast<float4v*>(dst + 16 * d + 4 * g) = O[h][d];
-            if (g == 0) *reinterpret_cast<float4v*>(dst + 128) = float4v{m[h], l[h], 0.f, 0.f};
+            // a query that saw no key in this split contributes nothing: report m = -inf-like
+            if (g == 0) *reinterpret_cast<float4v*>(dst + 128) = float4v{started[h] ? m[h] : kNoMax, l[h], 0.f, 0.f};
         }
     }
 }
@@ -280,7 +309,7 @@ __global__ __launch_bounds__(64) void attn_prefill_combine(const float* __restri
     dst[1] = O1 * inv;
 }
 
-constexpr int kNW = 2;  // waves per workgroup (16 queries each)
+constexpr int kNW = 4;  // waves per workgroup (16 queries each)
 
 template <int G>
 int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
