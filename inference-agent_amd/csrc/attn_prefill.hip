@@ -44,6 +44,7 @@ typedef __attribute__((address_space(3))) half8 lds_half8;
 
 constexpr int kBN = 64;                        // keys per tile
 constexpr float kLazy = 8.f;                   // base-2 headroom before the reference max moves
+constexpr int kBufferFlags = 0x00020000;       // buffer descriptor word 3 (raw, 32-bit format)
 constexpr int kRowBytes = kHeadDim * 2;        // 256 B per K/V row in LDS (no padding)
 constexpr int kTileBytes = kBN * kRowBytes;    // 16 KB per K or V tile
 constexpr int kStageBytes = 2 * kTileBytes;    // K + V
@@ -60,7 +61,8 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                          uint32_t n_head_kv, uint32_t n_splits, float qscale) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int li = lane & 15, g = lane >> 4;
     const uint32_t kvh = blockIdx.y, split = blockIdx.z;
     const size_t kv_dim = size_t(n_head_kv) * kHeadDim;
@@ -80,23 +82,37 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     const _Float16* Kg = K + size_t(kvh) * kHeadDim;
     const _Float16* Vg = V + size_t(kvh) * kHeadDim;
 
-    // Tile copy HBM -> LDS: 32 instructions of 1 KB (4 rows) per tile, spread over the waves.
-    // Lane l of an instruction fills physical chunk l%16 of row 4*i + l/16, so it fetches the
-    // logical chunk (l%16) ^ swizzle(row). Rows past kend are clamped to the last visible row
-    // (finite data; those keys are masked, so their P is exactly 0).
+    // Tile copy HBM -> LDS: 32 buffer_load ... lds instructions of 1 KB (4 rows) per tile,
+    // spread over the waves. Lane l of an instruction fills physical chunk l%16 of row
+    // 4*i + l/16, so it fetches the logical chunk (l%16) ^ swizzle(row). The per-lane byte
+    // offsets do not change from tile to tile; the buffer resource is rebased per tile and its
+    // size covers only the visible rows, so rows past kend read as zeros (finite; those keys
+    // are masked, so their P is exactly 0) with no clamping arithmetic.
+    constexpr int kInstPerWave = 32 / NW;
+    const uint32_t row_bytes = uint32_t(kv_dim) * 2;
+    uint32_t dma_off[kInstPerWave];
+#pragma unroll
+    for (int k = 0; k < kInstPerWave; k++) {
+        const int i = wave + k * NW;
+        const int isv = i >> 4;
+        const int row = 4 * (i & 15) + (lane >> 4);
+        const int logical = (lane & 15) ^ (isv ? swz_v(row) : swz_k(row));
+        dma_off[k] = uint32_t(row) * row_bytes + 16u * uint32_t(logical);
+    }
     auto issue_tile = [&](uint32_t t, int buf) {
         const uint32_t kb = t * kBN;
         char* stage = smem + buf * kStageBytes;
+        const uint32_t nrec = min(kend - kb, uint32_t(kBN)) * row_bytes;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(Kg + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>(Vg + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
 #pragma unroll
-        for (int i = wave; i < 32; i += NW) {
+        for (int k = 0; k < kInstPerWave; k++) {
+            const int i = wave + k * NW;  // wave-uniform
             const int isv = i >> 4;
-            const int row = 4 * (i & 15) + (lane >> 4);
-            const int phys = lane & 15;
-            const int logical = phys ^ (isv ? swz_v(row) : swz_k(row));
-            const uint32_t key = min(kb + row, kend - 1);
-            const _Float16* src = (isv ? Vg : Kg) + size_t(key) * kv_dim + 8 * logical;
             char* dst = stage + isv * kTileBytes + (4 * (i & 15)) * kRowBytes;
-            __builtin_amdgcn_global_load_lds(src, (lds_void*)dst, 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk, (lds_void*)dst, 16, int(dma_off[k]), 0, 0, 0);
         }
     };
 
