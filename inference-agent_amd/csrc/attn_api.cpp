@@ -59,7 +59,7 @@ uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
 
 uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
     if (check_prefill(d)) return 0;
-    return ingot::prefill_splits(d->pos, d->n_tok, d->n_head, d->n_splits);
+    return ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
 }
 
 size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
@@ -70,7 +70,7 @@ size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
 
 size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d) {
     if (check_prefill(d)) return 0;
-    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head, d->n_splits);
+    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
     const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head * kPartFloats * sizeof(float) : 0;
     return kCounterBytes + parts;
 }
@@ -106,7 +106,7 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
         !aligned16(workspace))
         return INGOT_ATTN_EINVAL;
     if (workspace_bytes < ingot_attn_prefill_workspace_size(d)) return INGOT_ATTN_EWORKSPACE;
-    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head, d->n_splits);
+    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
     auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
     const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;

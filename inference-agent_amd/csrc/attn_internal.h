@@ -17,7 +17,7 @@ constexpr uint32_t kCounterStride = 64;  // uint32 words
 constexpr size_t kCounterBytes = 65536;  // up to 256 KV heads
 
 uint32_t decode_splits(uint32_t n_keys, uint32_t n_head_kv, uint32_t requested);
-uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head, uint32_t requested);
+uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t requested);
 
 // Return 0, -2 (unsupported group) or -4 (launch failed).
 int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,

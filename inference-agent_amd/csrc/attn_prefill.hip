@@ -347,14 +347,16 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
 
 }  // namespace
 
-uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head, uint32_t requested) {
+uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t requested) {
     const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
     uint32_t splits = requested;
     if (splits == 0) {
-        // Aim for >= 2048 waves (2 per SIMD on 256 CUs), keeping >= 4 key tiles per split.
-        const uint32_t waves = ((n_tok + 15) / 16) * max(1u, n_head / 3);
-        splits = (2048 + waves - 1) / waves;
-        splits = min(splits, max(1u, max_tiles / 4));
+        // Two 4-wave workgroups per CU (2 waves/SIMD) need >= 512 workgroups on 256 CUs; split
+        // the key range when the query blocks alone give fewer, up to 4 ways (measured: more
+        // splits cost more in partial traffic than they gain), keeping >= 4 tiles per split.
+        const uint32_t wgs = ((n_tok + 16 * kNW - 1) / (16 * kNW)) * n_head_kv;
+        splits = (512 + wgs - 1) / wgs;
+        splits = min(min(splits, 4u), max(1u, max_tiles / 4));
     }
     return max(1u, min(splits, min(max_tiles, kMaxPrefillSplits)));
 }
