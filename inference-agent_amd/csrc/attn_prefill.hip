@@ -49,6 +49,18 @@ constexpr int kRowBytes = kHeadDim * 2;        // 256 B per K/V row in LDS (no p
 constexpr int kTileBytes = kBN * kRowBytes;    // 16 KB per K or V tile
 constexpr int kStageBytes = 2 * kTileBytes;    // K + V
 
+// Max over the 4 lanes l, l^16, l^32, l^48 (the lanes that hold one query column) with the
+// gfx950 lane-swap instructions: with both operands equal to x, the two results of
+// v_permlane16_swap are {x_l, x_(l^16)} and those of v_permlane32_swap {x_l, x_(l^32)}.
+__device__ __forceinline__ float max_lanes4(float x) {
+    unsigned u = __float_as_uint(x);
+    auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    x = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    u = __float_as_uint(x);
+    r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 // XOR swizzles of the 16-byte chunk index (0..15) inside a 256-byte row.
 __device__ __forceinline__ int swz_k(int row) { return row & 15; }       // A-operand row reads
 __device__ __forceinline__ int swz_v(int row) { return (row & 7) << 1; }  // transposing reads
@@ -158,14 +170,11 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         const char* Ks = smem + buf * kStageBytes;
         const char* Vs = Ks + kTileBytes;
 
-        // Two halves of 32 keys: scores, online-softmax update, then P*V for each half, so only
-        // 32 keys' worth of S and P is live at a time.
-#pragma unroll
-        for (int hs = 0; hs < 2; hs++) {
-            const uint32_t kh = kb + 32 * hs;
-            if (kh >= kend_w) break;
-            // S'^T = K Q^T - m: 2 key tiles of 16 x (G heads x 16 queries).
-            float4v S[2][G];
+        // Two halves of 32 keys (scores, online-softmax update, P*V each), so only 32 keys'
+        // worth of S and P is live at a time.
+        float4v S[2][G];
+        half8 P[G];
+        auto scores = [&](int hs) {
 #pragma unroll
             for (int T = 0; T < 2; T++) {
 #pragma unroll
@@ -180,6 +189,9 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                         S[T][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[h][ks], S[T][h], 0, 0, 0);
                 }
             }
+        };
+        auto softmax = [&](int hs) {
+            const uint32_t kh = kb + 32 * hs;
             // Causal mask where these keys reach past the wave's first query position.
             if (kh + 31 > pos + q0) {
 #pragma unroll
@@ -200,8 +212,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             for (int h = 0; h < G; h++) {
                 float x = fmaxf(fmaxf(fmaxf(S[0][h][0], S[0][h][1]), fmaxf(S[0][h][2], S[0][h][3])),
                                 fmaxf(fmaxf(S[1][h][0], S[1][h][1]), fmaxf(S[1][h][2], S[1][h][3])));
-                x = fmaxf(x, __shfl_xor(x, 16));
-                x = fmaxf(x, __shfl_xor(x, 32));
+                x = max_lanes4(x);
                 mx[h] = x;
                 grow_any |= started[h] ? (x > kLazy) : (x > -__builtin_inff());
             }
@@ -222,7 +233,6 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             }
             // P = 2^S' in f16 (P^T B operand: element 4T + j is key kh+16T+4g+j); row sums from
             // the same f16 values with v_dot2_f32_f16.
-            half8 P[G];
 #pragma unroll
             for (int h = 0; h < G; h++) {
 #pragma unroll
@@ -236,6 +246,8 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                     ls = __builtin_amdgcn_fdot2(half2v{P[h][2 * e], P[h][2 * e + 1]}, one, ls, false);
                 l[h] = ls;
             }
+        };
+        auto pv = [&](int hs, const half8 (&Pp)[G]) {
             // O^T (128 dims x (G x 16 queries)) += V^T (128 x 32) P^T (32 x 16) per head.
 #pragma unroll
             for (int d = 0; d < 8; d++) {
@@ -253,8 +265,17 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                 const half8 a = __builtin_shufflevector(part_[0], part_[1], 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
                 for (int h = 0; h < G; h++)
-                    O[h][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, P[h], O[h][d], 0, 0, 0);
+                    O[h][d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, Pp[h], O[h][d], 0, 0, 0);
             }
+        };
+
+        scores(0);
+        softmax(0);
+        pv(0, P);
+        if (kb + 32 < kend_w) {
+            scores(1);
+            softmax(1);
+            pv(1, P);
         }
     };
 
