@@ -5,8 +5,11 @@
 // steps (src/backend.h:16-20, src/cpu_backend.cpp:51-69) and of the reference's attn_prefill
 // (shaders/kernels.metal:518-633, mask `key <= pos+tok`, line 578), re-designed for CDNA4:
 //
-//   - A workgroup = NW waves over one KV head; wave w owns 16 queries and ALL G query heads of
-//     the group (48 score columns for G = 3). Every K/V operand read from LDS feeds G MFMAs
+//   - A workgroup = 8 waves over one KV head and 64 queries: 4 query waves x 2 key groups. A
+//     wave owns 16 queries and ALL G query heads of the group (48 score columns for G = 3);
+//     the two key groups take alternate key tiles (each with its own double-buffered LDS
+//     stages) and are merged through LDS at the end, which gives 2 waves per SIMD without
+//     splitting the key range across workgroups. Every K/V operand read from LDS feeds G MFMAs
 //     (v_mfma_f32_16x16x32_f16), so the GQA sharing happens at register level, on top of the
 //     workgroup-level sharing of each LDS tile.
 //   - K/V tiles (64 keys) are copied HBM -> LDS with global_load_lds (no VGPRs, no VALU) into a
@@ -65,8 +68,8 @@ __device__ __forceinline__ float max_lanes4(float x) {
 __device__ __forceinline__ int swz_k(int row) { return row & 15; }       // A-operand row reads
 __device__ __forceinline__ int swz_v(int row) { return (row & 7) << 1; }  // transposing reads
 
-template <int G, int NW>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(G == 4 ? 1 : 2)))
+template <int G, int QW, int KG>
+__global__ __launch_bounds__(64 * QW * KG) __attribute__((amdgpu_waves_per_eu(G == 4 ? 1 : 2)))
 void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict__ K,
                          const _Float16* __restrict__ V, float* __restrict__ out,
                          float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
@@ -75,14 +78,15 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+    const int qw = wave % QW, kg = wave / QW;  // query sub-block, key group
     const int li = lane & 15, g = lane >> 4;
     const uint32_t kvh = blockIdx.y, split = blockIdx.z;
     const size_t kv_dim = size_t(n_head_kv) * kHeadDim;
-    const uint32_t qblk0 = blockIdx.x * 16 * NW;
-    const uint32_t q0 = qblk0 + 16 * wave;
+    const uint32_t qblk0 = blockIdx.x * 16 * QW;
+    const uint32_t q0 = qblk0 + 16 * qw;
 
     // Keys [0, kend) are visible to some query of this workgroup.
-    const uint32_t qlast_wg = min(n_tok, qblk0 + 16 * NW) - 1;
+    const uint32_t qlast_wg = min(n_tok, qblk0 + 16 * QW) - 1;
     const uint32_t kend = pos + qlast_wg + 1;
     const uint32_t ntiles = (kend + kBN - 1) / kBN;
     const uint32_t t_begin = uint32_t((uint64_t(split) * ntiles) / n_splits);
@@ -100,12 +104,12 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // offsets do not change from tile to tile; the buffer resource is rebased per tile and its
     // size covers only the visible rows, so rows past kend read as zeros (finite; those keys
     // are masked, so their P is exactly 0) with no clamping arithmetic.
-    constexpr int kInstPerWave = 32 / NW;
+    constexpr int kInstPerWave = 32 / QW;  // each key group copies its own tiles
     const uint32_t row_bytes = uint32_t(kv_dim) * 2;
     uint32_t dma_off[kInstPerWave];
 #pragma unroll
     for (int k = 0; k < kInstPerWave; k++) {
-        const int i = wave + k * NW;
+        const int i = qw + k * QW;
         const int isv = i >> 4;
         const int row = 4 * (i & 15) + (lane >> 4);
         const int logical = (lane & 15) ^ (isv ? swz_v(row) : swz_k(row));
@@ -113,7 +117,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     }
     auto issue_tile = [&](uint32_t t, int buf) {
         const uint32_t kb = t * kBN;
-        char* stage = smem + buf * kStageBytes;
+        char* stage = smem + (kg * 2 + buf) * kStageBytes;
         const uint32_t nrec = min(kend - kb, uint32_t(kBN)) * row_bytes;
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<_Float16*>(Kg + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
@@ -121,7 +125,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             const_cast<_Float16*>(Vg + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
 #pragma unroll
         for (int k = 0; k < kInstPerWave; k++) {
-            const int i = wave + k * NW;  // wave-uniform
+            const int i = qw + k * QW;  // wave-uniform
             const int isv = i >> 4;
             char* dst = stage + isv * kTileBytes + (4 * (i & 15)) * kRowBytes;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk, (lds_void*)dst, 16, int(dma_off[k]), 0, 0, 0);
@@ -167,7 +171,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     auto compute_tile = [&](uint32_t t, int buf) {
         const uint32_t kb = t * kBN;
         if (kb >= kend_w) return;  // every key of this tile is in this wave's future
-        const char* Ks = smem + buf * kStageBytes;
+        const char* Ks = smem + (kg * 2 + buf) * kStageBytes;
         const char* Vs = Ks + kTileBytes;
 
         // Two halves of 32 keys (scores, online-softmax update, P*V each), so only 32 keys'
@@ -279,18 +283,59 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         }
     };
 
+    // Key group kg takes tiles t_begin + kg, t_begin + kg + KG, ...; all groups step together
+    // (one barrier per step).
     if (t_begin < t_end) {
-        issue_tile(t_begin, 0);
+        const uint32_t steps = (t_end - t_begin + KG - 1) / KG;
+        uint32_t t = t_begin + kg;
+        if (t < t_end) issue_tile(t, 0);
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         int buf = 0;
-        for (uint32_t t = t_begin; t < t_end; t++) {
-            if (t + 1 < t_end) issue_tile(t + 1, buf ^ 1);
-            compute_tile(t, buf);
-            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile t+1 have landed
-            __syncthreads();                // ... and everyone's; tile t is no longer read
+        for (uint32_t st = 0; st < steps; st++, t += KG) {
+            if (t + KG < t_end) issue_tile(t + KG, buf ^ 1);
+            if (t < t_end) compute_tile(t, buf);
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of the next tile have landed
+            __syncthreads();                // ... and everyone's; this tile is no longer read
             buf ^= 1;
         }
+    }
+
+    if (KG == 2) {
+        // Merge the two key groups through LDS (the tiles are no longer read), one head at a
+        // time: group 1 stores its (O, m, l, started) per lane, group 0 folds it in with the
+        // log-sum-exp rule. 35 words x 64 lanes x QW waves per round.
+        constexpr int kFields = 32 + 3;
+        float* st = reinterpret_cast<float*>(smem) + qw * kFields * 64 + lane;
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            if (kg == 1) {
+#pragma unroll
+                for (int d = 0; d < 8; d++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) st[(d * 4 + j) * 64] = O[h][d][j];
+                st[32 * 64] = m[h];
+                st[33 * 64] = l[h];
+                st[34 * 64] = started[h] ? 1.f : 0.f;
+            }
+            __syncthreads();
+            if (kg == 0) {
+                const float m1 = st[32 * 64], l1 = st[33 * 64];
+                const bool s1 = st[34 * 64] != 0.f;
+                const float M = started[h] ? (s1 ? fmaxf(m[h], m1) : m[h]) : m1;
+                const float a0 = started[h] ? fast_exp2(m[h] - M) : 0.f;
+                const float a1 = s1 ? fast_exp2(m1 - M) : 0.f;
+#pragma unroll
+                for (int d = 0; d < 8; d++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) O[h][d][j] = O[h][d][j] * a0 + st[(d * 4 + j) * 64] * a1;
+                l[h] = l[h] * a0 + l1 * a1;
+                m[h] = (started[h] || s1) ? M : m[h];
+                started[h] = started[h] || s1;
+            }
+            __syncthreads();
+        }
+        if (kg == 1) return;
     }
 
     // Row sums: the 4 lane groups g hold partial sums of the same query (same m).
@@ -346,16 +391,21 @@ __global__ __launch_bounds__(64) void attn_prefill_combine(const float* __restri
     dst[1] = O1 * inv;
 }
 
-constexpr int kNW = 4;  // waves per workgroup (16 queries each)
+constexpr int kQW = 4;  // query waves per workgroup (16 queries x G heads each)
+constexpr int kKG = 2;  // key groups per workgroup (alternate tiles, merged through LDS)
 
 template <int G>
 int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                      uint32_t n_splits, float qscale, hipStream_t stream) {
-    const dim3 grid((n_tok + 16 * kNW - 1) / (16 * kNW), n_head_kv, n_splits);
-    const size_t lds = 2 * kStageBytes;
-    hipLaunchKernelGGL((attn_prefill_kernel<G, kNW>), grid, dim3(64 * kNW), lds, stream, q, k, v,
-                       out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale);
+    const dim3 grid((n_tok + 16 * kQW - 1) / (16 * kQW), n_head_kv, n_splits);
+    const size_t lds = size_t(kKG) * 2 * kStageBytes;  // 128 KB: two double-buffered stages
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&attn_prefill_kernel<G, kQW, kKG>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+    if (attr != hipSuccess) return -4;
+    hipLaunchKernelGGL((attn_prefill_kernel<G, kQW, kKG>), grid, dim3(64 * kQW * kKG), lds, stream,
+                       q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale);
     if (hipGetLastError() != hipSuccess) return -4;
     if (n_splits > 1) {
         const uint32_t n_head = n_head_kv * G;
@@ -372,12 +422,12 @@ uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32
     const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
     uint32_t splits = requested;
     if (splits == 0) {
-        // Two 4-wave workgroups per CU (2 waves/SIMD) need >= 512 workgroups on 256 CUs; split
+        // One 8-wave workgroup per CU (2 waves/SIMD) needs >= 256 workgroups on 256 CUs; split
         // the key range when the query blocks alone give fewer, up to 4 ways (measured: more
-        // splits cost more in partial traffic than they gain), keeping >= 4 tiles per split.
-        const uint32_t wgs = ((n_tok + 16 * kNW - 1) / (16 * kNW)) * n_head_kv;
-        splits = (512 + wgs - 1) / wgs;
-        splits = min(min(splits, 4u), max(1u, max_tiles / 4));
+        // splits cost more in partial traffic than they gain), keeping >= 8 tiles per split.
+        const uint32_t wgs = ((n_tok + 16 * kQW - 1) / (16 * kQW)) * n_head_kv;
+        splits = (256 + wgs - 1) / wgs;
+        splits = min(min(splits, 4u), max(1u, max_tiles / 8));
     }
     return max(1u, min(splits, min(max_tiles, kMaxPrefillSplits)));
 }
