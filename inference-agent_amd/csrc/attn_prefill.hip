@@ -158,11 +158,14 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // reference, so this is exact.
     float4v O[G][8];
     float m[G], l[G];
+    float4v negm[G];  // {-m, -m, -m, -m}: the C operand of the first score MFMA of each tile
     bool started[G];
+    bool all_started = false;  // wave-uniform: every lane has seen a key for every head
 #pragma unroll
     for (int h = 0; h < G; h++) {
         m[h] = 0.f;
         l[h] = 0.f;
+        negm[h] = float4v{0.f, 0.f, 0.f, 0.f};
         started[h] = false;
 #pragma unroll
         for (int d = 0; d < 8; d++) O[h][d] = float4v{0.f, 0.f, 0.f, 0.f};
@@ -181,8 +184,6 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         auto scores = [&](int hs) {
 #pragma unroll
             for (int T = 0; T < 2; T++) {
-#pragma unroll
-                for (int h = 0; h < G; h++) S[T][h] = float4v{-m[h], -m[h], -m[h], -m[h]};
                 const int row = 32 * hs + 16 * T + li;
 #pragma unroll
                 for (int ks = 0; ks < 4; ks++) {
@@ -190,7 +191,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                     const half8 a = *reinterpret_cast<const lds_half8*>((const lds_void*)(Ks + row * kRowBytes + 16 * chunk));
 #pragma unroll
                     for (int h = 0; h < G; h++)
-                        S[T][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[h][ks], S[T][h], 0, 0, 0);
+                        S[T][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[h][ks], ks == 0 ? negm[h] : S[T][h], 0, 0, 0);
                 }
             }
         };
@@ -209,31 +210,41 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                         }
                     }
             }
-            // Per head: does the reference max have to move? (max over the 4 lanes of a query)
-            float mx[G];
-            bool grow_any = false;
+            // Does a reference max have to move? In steady state (every lane started) one
+            // max over all G*8 scores of the lane and a ballot decide; the exact per-head
+            // cross-lane max is computed only when something moves or some lane has not seen
+            // a key yet.
+            bool need = true;
+            if (all_started) {
+                float x = -__builtin_inff();
 #pragma unroll
-            for (int h = 0; h < G; h++) {
-                float x = fmaxf(fmaxf(fmaxf(S[0][h][0], S[0][h][1]), fmaxf(S[0][h][2], S[0][h][3])),
-                                fmaxf(fmaxf(S[1][h][0], S[1][h][1]), fmaxf(S[1][h][2], S[1][h][3])));
-                x = max_lanes4(x);
-                mx[h] = x;
-                grow_any |= started[h] ? (x > kLazy) : (x > -__builtin_inff());
+                for (int h = 0; h < G; h++)
+#pragma unroll
+                    for (int T = 0; T < 2; T++)
+                        x = fmaxf(x, fmaxf(fmaxf(S[T][h][0], S[T][h][1]), fmaxf(S[T][h][2], S[T][h][3])));
+                need = __builtin_amdgcn_ballot_w64(x > kLazy) != 0;
             }
-            if (__builtin_amdgcn_ballot_w64(grow_any)) {  // wave-uniform, rare after warm-up
+            if (need) {  // wave-uniform, rare after warm-up
+                bool pending = false;
 #pragma unroll
                 for (int h = 0; h < G; h++) {
-                    const bool grow = started[h] ? (mx[h] > kLazy) : (mx[h] > -__builtin_inff());
-                    const float delta = grow ? mx[h] : 0.f;
+                    float x = fmaxf(fmaxf(fmaxf(S[0][h][0], S[0][h][1]), fmaxf(S[0][h][2], S[0][h][3])),
+                                    fmaxf(fmaxf(S[1][h][0], S[1][h][1]), fmaxf(S[1][h][2], S[1][h][3])));
+                    x = max_lanes4(x);  // max over the 4 lanes of a query
+                    const bool grow = started[h] ? (x > kLazy) : (x > -__builtin_inff());
+                    const float delta = grow ? x : 0.f;
                     const float alpha = fast_exp2(-delta);
                     m[h] += delta;
+                    negm[h] = float4v{-m[h], -m[h], -m[h], -m[h]};
                     l[h] *= alpha;
                     started[h] |= grow;
+                    pending |= !started[h];
 #pragma unroll
                     for (int T = 0; T < 2; T++) S[T][h] -= delta;
 #pragma unroll
                     for (int d = 0; d < 8; d++) O[h][d] *= alpha;
                 }
+                all_started = __builtin_amdgcn_ballot_w64(pending) == 0;
             }
             // P = 2^S' in f16 (P^T B operand: element 4T + j is key kh+16T+4g+j); row sums from
             // the same f16 values with v_dot2_f32_f16.
