@@ -24,7 +24,8 @@ int check_common(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
     if (head_dim != 128) return INGOT_ATTN_EUNSUPPORTED;
     const uint32_t group = n_head / n_head_kv;
     if (group < 1 || group > 4) return INGOT_ATTN_EUNSUPPORTED;
-    if (n_head_kv > kCounterBytes / (ingot::kCounterStride * sizeof(unsigned int))) return INGOT_ATTN_EUNSUPPORTED;
+    // One completion counter per query head (decode) or KV head (prefill).
+    if (n_head > kCounterBytes / (ingot::kCounterStride * sizeof(unsigned int))) return INGOT_ATTN_EUNSUPPORTED;
     return INGOT_ATTN_OK;
 }
 

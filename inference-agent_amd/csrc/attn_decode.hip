@@ -3,39 +3,55 @@
 // Computes, for one query token and every Q head h, out_h = softmax(q_h K^T * scale) V over cache
 // rows 0..n_keys-1 of KV head h / G — the attention block of src/cpu_backend.cpp:51-69 and the
 // decode flash path of src/metal_backend.mm:339-359 (attn_decode_g3 + attn_combine,
-// shaders/kernels.metal:428-516), re-designed for CDNA4:
+// shaders/kernels.metal:428-516), re-designed for CDNA4.
 //
-//   grid (n_splits, n_head_kv), NW wave64s per workgroup. A workgroup owns one KV head and one
-//   contiguous key slice and serves all G query heads of the group from each K/V row it reads.
-//   A wave step covers 16 keys:
+// Grid: one dimension of n_splits * n_head_kv workgroups, workgroup b serving KV head
+// b % n_head_kv and key slice b / n_head_kv. The hardware hands workgroups to the 8 XCDs round
+// robin (b % 8), so with 8 KV heads every slice of one KV head runs on the same XCD and its
+// records meet in one L2. Each workgroup has NW wave64s; a wave step covers 16 keys and serves all
+// G query heads of the group from each K/V row it reads:
 //   - Scores on the matrix cores: S (16 rows x 16 keys) = A (16 x 256) * B (256 x 16) with
 //     v_mfma_f32_16x16x32_f16 x 8. Rows 0..G-1 of A hold the G query heads; the 256-long
 //     contraction is q_hi (128 dims) followed by q_lo (128 dims), where q*scale*log2(e) =
 //     q_hi + q_lo with both parts f16, and B is the K tile repeated twice (same registers). The
-//     score is thus exact to ~2^-22 relative even though K and the MFMA inputs are f16; the
+//     score is thus exact to ~2^-22 relative although K and the MFMA inputs are f16; the
 //     accumulation is f32. Lane l loads 4 x 16 bytes of key row l%16.
 //   - Online softmax per head with a wave-uniform running max (base 2), 16-lane DPP max.
-//   - P*V on the vector ALUs (v_fma_mix: f16 V, f32 P and accumulators). For this, lane l owns
-//     dims 8*(l%16)..+7 of key rows l/16 + 4u (u = 0..3); p reaches it through LDS.
+//   - P*V on the vector ALUs (v_fma_mix: f16 V, f32 P and accumulators). Lane l owns dims
+//     8*(l%16)..+7 of key rows l/16 + 4u (u = 0..3); p reaches it through LDS.
 //   - The K and V loads of the next step are issued before the current step is computed.
-//   Waves merge through LDS. Splits merge in the last workgroup to finish for a KV head (a
-//   completion counter, so no second launch; the reference launches attn_combine separately).
-//   Partial records are written and read with device-scope (sc1) accesses, so neither an L2
-//   writeback nor an L2 invalidate is needed; the merging workgroup issues all its loads in
-//   one batch and spreads the splits over all of its threads.
+//
+// The tail is latency, not bandwidth: after the last K/V row arrives, what is left is a chain of
+// device-memory round trips, so it is cut per query head. Each wave publishes its four lane-group
+// partials of o (no cross-lane reduction) and its (m, l) in LDS; after one barrier, wave h (h < G)
+// alone merges head h of the workgroup, stores the head's record (o[128], m, l) with 16-byte
+// device-scope stores, waits for them, and bumps the head's completion counter. The last slice to
+// arrive for a head merges that head's n_splits records: lane (half, j) loads 16-byte chunk j of
+// the records of splits half, half + 2, ...; lane t loads (m, l) of split t, the wave reduces the
+// maximum, each lane computes its split's weight once, and the weights reach the chunk owners
+// through LDS. The three heads of a group thus merge in parallel, in three different waves, with
+// no workgroup barrier after the counter. Device-scope (sc1) accesses make the records visible
+// across XCDs without an L2 writeback or invalidate, whatever the workgroup placement.
 //
 // MFMA 16x16x32 f16 register layouts (wave64, lane l, i = l%16, g = l/16):
 //   A (16 x 32): lane holds A[i][8g + e], e = 0..7;  B (32 x 16): lane holds B[8g + e][i];
 //   D (16 x 16): lane holds D[4g + j][i], j = 0..3.
 //
-// Partial record (per KV head, split, group head): o[128] (unnormalized), m, l — as the
-// reference's part[...][130] (AD_STRIDE, shaders/kernels.metal:291), stride 132 here.
+// Record layout (workspace, after the counters): [head][split][kPartStride] with o[128]
+// (unnormalized, relative to m), m (base 2), l — the reference's part[...][130] record
+// (AD_STRIDE, shaders/kernels.metal:291) with stride 132.
 #include "attn_common.h"
 #include "attn_internal.h"
 
 namespace ingot {
 
 namespace {
+
+constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw, 32-bit format)
+constexpr int kScDevice = 16;             // buffer cache-policy bits: sc1 = device scope
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float row16_max(float x) {
     x = fmaxf(x, dpp<0xB1>(x));
@@ -49,29 +65,68 @@ __device__ __forceinline__ float lane0(float x) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
 }
 
+// With both operands equal to x, the two results of v_permlane16_swap are {x_l, x_(l^16)} and
+// those of v_permlane32_swap {x_l, x_(l^32)} (gfx950 lane-swap instructions).
+__device__ __forceinline__ float sum_x16(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_x32(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_x16(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_x32(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <int G, int NW>
 __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
     float* __restrict__ out, float* __restrict__ part, unsigned int* __restrict__ counters,
     uint32_t n_keys, uint32_t keys_per_split, uint32_t n_splits, uint32_t n_head_kv,
     float qscale) {
-    constexpr int NT = 64 * NW;
+    static_assert(G <= NW, "one tail wave per query head of the group");
+    static_assert(kMaxDecodeSplits <= 64, "one lane per split in the merge");
     constexpr int KW = 16;  // keys per wave step
-    // LDS: per-wave records during the workgroup merge, then per-thread partial merges in the
-    // cross-split merge (the two uses do not overlap in time).
-    constexpr int kRedFloats = NW * G * kPartStride;
-    constexpr int kMrgFloats = NT * 6;
-    __shared__ __attribute__((aligned(16))) float lds[kRedFloats > kMrgFloats ? kRedFloats : kMrgFloats];
+    constexpr int ITER = int(kMaxDecodeSplits) / 2;
+    __shared__ __attribute__((aligned(16))) float lds_o[NW][4][G][kHeadDim];  // per lane group r
+    __shared__ float lds_ml[NW][G][2];
     __shared__ __attribute__((aligned(16))) float lds_p[NW][KW][4];  // p[key][head] per wave
-    __shared__ int s_last;
+    __shared__ float lds_w[G][64];                                   // split weights per head
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane >> 4, c = lane & 15;
-    const uint32_t split = blockIdx.x, kvh = blockIdx.y;
+    const uint32_t kvh = blockIdx.x % n_head_kv, split = blockIdx.x / n_head_kv;
     const size_t kv_dim = size_t(n_head_kv) * kHeadDim;
     const uint32_t k0 = split * keys_per_split;
     const uint32_t k1 = min(n_keys, k0 + keys_per_split);
+
+    // K: lane reads key row (base + c), 16 bytes at dims 32m + 8r. V: key rows base + 4u + r,
+    // 16 bytes at dims 8c. Loads are unconditional: rows past the slice are clamped to its last
+    // row (already in cache), so the number of loads in flight is the same on every path and
+    // the compiler's wait counts never stall the current step on the prefetch of the next.
+    const _Float16* Kb = K + size_t(kvh) * kHeadDim + 8 * r;
+    const _Float16* Vb = V + size_t(kvh) * kHeadDim + 8 * c;
+    auto load_step = [&](uint32_t b, half8 (&kx)[4], half8 (&vx)[4]) {
+        const uint32_t kk = min(b + c, k1 - 1);
+#pragma unroll
+        for (int m = 0; m < 4; m++) kx[m] = load_half8(Kb + size_t(kk) * kv_dim + 32 * m);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t kv = min(b + 4 * u + r, k1 - 1);
+            vx[u] = load_half8(Vb + size_t(kv) * kv_dim);
+        }
+    };
 
     // A operand: lane holds A[row c][k = 8r + e] of MFMA m (m < 4: q_hi of dims 32m+8r+e,
     // m >= 4: q_lo of the same dims). Rows >= G are zero.
@@ -103,25 +158,6 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         for (int i = 0; i < 8; i++) o[h][i] = 0.f;
     }
 
-    // K: lane reads key row (base + c), 16 bytes at dims 32m + 8r. V: key rows base + 4u + r,
-    // 16 bytes at dims 8c.
-    const _Float16* Kb = K + size_t(kvh) * kHeadDim + 8 * r;
-    const _Float16* Vb = V + size_t(kvh) * kHeadDim + 8 * c;
-
-    // Loads are unconditional: rows past the slice are clamped to its last row (already in
-    // cache), so the number of loads in flight is the same on every path and the compiler's
-    // wait counts never stall the current step on the prefetch of the next. Two register
-    // buffers alternate (ping-pong), so a prefetch never waits for the step it follows.
-    auto load_step = [&](uint32_t b, half8 (&kx)[4], half8 (&vx)[4]) {
-        const uint32_t kk = min(b + c, k1 - 1);
-#pragma unroll
-        for (int m = 0; m < 4; m++) kx[m] = load_half8(Kb + size_t(kk) * kv_dim + 32 * m);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const uint32_t kv = min(b + 4 * u + r, k1 - 1);
-            vx[u] = load_half8(Vb + size_t(kv) * kv_dim);
-        }
-    };
     auto compute_step = [&](uint32_t b, const half8 (&kx)[4], const half8 (&vx)[4]) {
         // S[row][key]: lane holds rows 4r..4r+3 of key c; rows 0..G-1 (lanes 0..15) are real.
         float4v S = {0.f, 0.f, 0.f, 0.f};
@@ -158,6 +194,8 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         __builtin_amdgcn_wave_barrier();
     };
 
+    // Two register buffers alternate (ping-pong), so a prefetch never waits for the step it
+    // follows.
     constexpr uint32_t kStride = NW * KW;
     uint32_t base = k0 + wave * KW;
     half8 ka[4], va[4], kb[4], vb[4];
@@ -174,172 +212,110 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         base += kStride;
     }
 
-    // Wave totals: o summed over the 4 lane rows (same dims, same wave-uniform max); l summed
-    // over lanes 0..15.
+    // Publish the wave's partials: lane group r holds dims 8c..8c+7 of its key rows; all four
+    // groups share the wave-uniform m, so the reader sums them without weights.
 #pragma unroll
     for (int h = 0; h < G; h++) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float x = o[h][i];
-            x += __shfl_xor(x, 16);
-            x += __shfl_xor(x, 32);
-            o[h][i] = x;
-        }
-        l_run[h] = row16_sum(r == 0 ? l_run[h] : 0.f);
-    }
-    if (r == 0) {
-#pragma unroll
-        for (int h = 0; h < G; h++) {
-            float* rec = lds + (wave * G + h) * kPartStride;
-            *reinterpret_cast<float4v*>(rec + 8 * c) = float4v{o[h][0], o[h][1], o[h][2], o[h][3]};
-            *reinterpret_cast<float4v*>(rec + 8 * c + 4) = float4v{o[h][4], o[h][5], o[h][6], o[h][7]};
-            if (c == 0) {
-                rec[128] = m_run[h];
-                rec[129] = l_run[h];
-            }
+        float* dst = &lds_o[wave][r][h][8 * c];
+        *reinterpret_cast<float4v*>(dst) = float4v{o[h][0], o[h][1], o[h][2], o[h][3]};
+        *reinterpret_cast<float4v*>(dst + 4) = float4v{o[h][4], o[h][5], o[h][6], o[h][7]};
+        const float l = row16_sum(r == 0 ? l_run[h] : 0.f);
+        if (lane == 0) {
+            lds_ml[wave][h][0] = m_run[h];
+            lds_ml[wave][h][1] = l;
         }
     }
     __syncthreads();
+    if (wave >= G) return;
 
-    // Merge the waves: thread t < G*32 owns head t/32, dims 4*(t%32)..+3.
-    if (tid < G * 32) {
-        const int h = tid >> 5, d = (tid & 31) * 4;
-        float M = kNoMax;
+    // Wave h merges head h of this workgroup; lane j < 32 owns dims 4j..4j+3.
+    const int h = wave, j = lane & 31;
+    float M = kNoMax;
 #pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, lds[(w * G + h) * kPartStride + 128]);
-        float L = 0.f;
-        float4v O = {0.f, 0.f, 0.f, 0.f};
+    for (int w = 0; w < NW; w++) M = fmaxf(M, lds_ml[w][h][0]);
+    float L = 0.f;
+    float4v O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float* rec = lds + (w * G + h) * kPartStride;
-            const float wt = fast_exp2(rec[128] - M);
-            L += rec[129] * wt;
-            O += *reinterpret_cast<const float4v*>(rec + d) * wt;
-        }
-        const size_t head = size_t(kvh) * G + h;
-        if (n_splits == 1) {
-            const float inv = L > 0.f ? 1.f / L : 0.f;
-            *reinterpret_cast<float4v*>(out + head * kHeadDim + d) = O * inv;
-        } else {
-            // Device-scope (sc1) stores, all issued before one wait for their completion, so
-            // the record is visible to a workgroup on another XCD without an L2 writeback.
-            float* dst = part + ((size_t(kvh) * n_splits + split) * G + h) * kPartStride;
+    for (int w = 0; w < NW; w++) {
+        const float wt = fast_exp2(lds_ml[w][h][0] - M);
+        L += lds_ml[w][h][1] * wt;
+        float4v s4 = *reinterpret_cast<const float4v*>(&lds_o[w][0][h][4 * j]);
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                __hip_atomic_store(dst + d + i, O[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (d == 0) {
-                __hip_atomic_store(dst + 128, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(dst + 129, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-            __builtin_amdgcn_s_waitcnt(0);  // the device-scope stores have completed
-        }
+        for (int g = 1; g < 4; g++) s4 += *reinterpret_cast<const float4v*>(&lds_o[w][g][h][4 * j]);
+        O += s4 * wt;
     }
-    if (n_splits == 1) return;
+    const size_t head = size_t(kvh) * G + h;
+    if (n_splits == 1) {
+        if (lane < 32)
+            *reinterpret_cast<float4v*>(out + head * kHeadDim + 4 * j) = O * (L > 0.f ? 1.f / L : 0.f);
+        return;
+    }
 
-    // The last workgroup to finish for this KV head merges the n_splits partials. The records
-    // were stored device-scope and awaited before the barrier, so a relaxed device-scope
-    // counter increment orders them; only the merging workgroup invalidates its L2 (acquire).
-    unsigned int* counter = counters + size_t(kvh) * kCounterStride;
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_last = (prev == n_splits - 1);
-    }
-    __syncthreads();
-    if (!s_last) return;
+    // This head's record for this split: 16-byte device-scope stores, awaited before the count.
+    const uint32_t rec_bytes = kPartStride * 4;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        part, 0, uint32_t(n_head_kv * G * n_splits * rec_bytes), kBufferFlags);
+    const int rec0 = int(head * n_splits * rec_bytes);  // byte offset of split 0's record
+    if (lane < 32)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), prs,
+                                               rec0 + int(split * rec_bytes) + 16 * j, 0, kScDevice);
+    if (lane == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(M), __float_as_uint(L)}, prs,
+                                              rec0 + int(split * rec_bytes) + 512, 0, kScDevice);
+    __builtin_amdgcn_s_waitcnt(0);  // the records have reached device scope
 
-    // Merge: thread t < P*COLS owns column (head, 4 dims) t % COLS and the splits s = t / COLS
-    // (mod P). All of its record words are loaded device-scope (sc1, coherent across XCDs
-    // without an L2 invalidate) in one unrolled batch, merged with the log-sum-exp rule, and
-    // the P partial merges per column are combined through LDS.
-    {
-        constexpr int COLS = G * 32;
-        constexpr int P = NT / COLS;
-        constexpr int ITER = (int(kMaxDecodeSplits) + P - 1) / P;
-        float M = kNoMax, L = 0.f;
-        float4v O = {0.f, 0.f, 0.f, 0.f};
-        const int col = tid % COLS, grp = tid / COLS;
-        const int h = col >> 5, d = (col & 31) * 4;
-        if (grp < P) {
-            const float* base_rec = part + (size_t(kvh) * n_splits * G + h) * kPartStride;
-            float ms[ITER], ls[ITER];
-            float4v os[ITER];
-            // Unconditional loads from clamped indices (no branches between them, so they
-            // are all in flight at once); out-of-range splits are masked afterwards.
+    unsigned int* counter = counters + head * kCounterStride;
+    unsigned prev = 0;
+    if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __builtin_amdgcn_readfirstlane(prev);
+    if (prev != n_splits - 1) return;
+
+    // Last arriver for this head: merge the n_splits records. Loads are unconditional from
+    // clamped split indices so they are all in flight at once; splits past n_splits get weight 0.
+    const int half = lane >> 5;
+    float4v os[ITER];
 #pragma unroll
-            for (int it = 0; it < ITER; it++) {
-                const uint32_t sp = min(uint32_t(grp + it * P), n_splits - 1);
-                const float* rec = base_rec + size_t(sp) * G * kPartStride;
-                ms[it] = __hip_atomic_load(rec + 128, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                ls[it] = __hip_atomic_load(rec + 129, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    os[it][i] = __hip_atomic_load(rec + d + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-#pragma unroll
-            for (int it = 0; it < ITER; it++) {
-                const bool ok = uint32_t(grp + it * P) < n_splits;
-                ms[it] = ok ? ms[it] : kNoMax;
-                ls[it] = ok ? ls[it] : 0.f;
-                os[it] = ok ? os[it] : float4v{0.f, 0.f, 0.f, 0.f};
-            }
-#pragma unroll
-            for (int it = 0; it < ITER; it++) M = fmaxf(M, ms[it]);
-#pragma unroll
-            for (int it = 0; it < ITER; it++) {
-                const float wt = fast_exp2(ms[it] - M);
-                L += ls[it] * wt;
-                O += os[it] * wt;
-            }
-        }
-        __syncthreads();  // the workgroup-merge records in LDS are no longer needed
-        float* red = lds;  // [P][COLS][6]: o[4], m, l
-        if (grp < P) {
-            float* e = red + (grp * COLS + col) * 6;
-            e[0] = O[0]; e[1] = O[1]; e[2] = O[2]; e[3] = O[3]; e[4] = M; e[5] = L;
-        }
-        __syncthreads();
-        if (tid < COLS) {
-            float Mt = kNoMax;
-#pragma unroll
-            for (int g = 0; g < P; g++) Mt = fmaxf(Mt, red[(g * COLS + tid) * 6 + 4]);
-            float Lt = 0.f;
-            float4v Ot = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int g = 0; g < P; g++) {
-                const float* e = red + (g * COLS + tid) * 6;
-                const float wt = fast_exp2(e[4] - Mt);
-                Lt += e[5] * wt;
-                Ot += float4v{e[0], e[1], e[2], e[3]} * wt;
-            }
-            const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
-            *reinterpret_cast<float4v*>(out + (size_t(kvh) * G + h) * kHeadDim + d) = Ot * inv;
-        }
+    for (int i = 0; i < ITER; i++) {
+        const uint32_t sp = min(uint32_t(half + 2 * i), n_splits - 1);
+        os[i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                prs, rec0 + int(sp * rec_bytes) + 16 * j, 0, kScDevice));
     }
-    if (tid == 0)  // leave the workspace ready for the next call
+    const uint32_t st = min(uint32_t(lane), n_splits - 1);
+    const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, rec0 + int(st * rec_bytes) + 512, 0, kScDevice);
+    const float m_s = uint32_t(lane) < n_splits ? __uint_as_float(ml[0]) : kNoMax;
+    const float Mt = max_x32(max_x16(row16_max(m_s)));
+    const float w = fast_exp2(m_s - Mt);  // 0 for lanes past n_splits
+    const float Lt = sum_x32(sum_x16(row16_sum(w * __uint_as_float(ml[1]))));
+    lds_w[h][lane] = w;
+    __builtin_amdgcn_wave_barrier();
+    float4v Ot = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < ITER; i++) Ot += os[i] * lds_w[h][half + 2 * i];
+#pragma unroll
+    for (int e = 0; e < 4; e++) Ot[e] = sum_x32(Ot[e]);
+    if (lane < 32)
+        *reinterpret_cast<float4v*>(out + head * kHeadDim + 4 * j) = Ot * (Lt > 0.f ? 1.f / Lt : 0.f);
+    if (lane == 0)  // leave the workspace ready for the next call
         __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int G, int NW>
-void launch_g(dim3 grid, hipStream_t stream, const float* q, const _Float16* k, const _Float16* v,
-              float* out, float* part, unsigned int* counters, uint32_t n_keys, uint32_t per,
-              uint32_t n_splits, uint32_t n_head_kv, float qscale) {
-    hipLaunchKernelGGL((attn_decode_kernel<G, NW>), grid, dim3(64 * NW), 0, stream, q, k, v, out,
-                       part, counters, n_keys, per, n_splits, n_head_kv, qscale);
+void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
+              const _Float16* v, float* out, float* part, unsigned int* counters, uint32_t n_keys,
+              uint32_t per, uint32_t n_splits, uint32_t n_head_kv, float qscale) {
+    hipLaunchKernelGGL((attn_decode_kernel<G, NW>), dim3(n_blocks), dim3(64 * NW), 0, stream, q, k,
+                       v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale);
 }
 
 constexpr int kNW = 4;
-constexpr uint32_t kKeysPerBlockStep = uint32_t(kNW) * 16;
+constexpr uint32_t kMinKeysPerSplit = 32;  // two wave steps: the tail costs more than the loads
 
 }  // namespace
 
 uint32_t decode_splits(uint32_t n_keys, uint32_t n_head_kv, uint32_t requested) {
     (void)n_head_kv;
     uint32_t splits = requested;
-    if (splits == 0) {
-        // One block step (kKeysPerBlockStep keys) or more per workgroup.
-        splits = (n_keys + kKeysPerBlockStep - 1) / kKeysPerBlockStep;
-    }
+    if (splits == 0) splits = (n_keys + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
     splits = max(1u, min(splits, min(n_keys, kMaxDecodeSplits)));
     // No empty splits: recompute from the per-split key count.
     const uint32_t per = (n_keys + splits - 1) / splits;
@@ -350,13 +326,13 @@ int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* o
                   unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
                   uint32_t group, float scale, hipStream_t stream) {
     const uint32_t per = (n_keys + n_splits - 1) / n_splits;
-    const dim3 grid(n_splits, n_head_kv);
+    const uint32_t blocks = n_splits * n_head_kv;
     const float qscale = scale * kLog2e;
     switch (group) {
-        case 1: launch_g<1, kNW>(grid, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 2: launch_g<2, kNW>(grid, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 3: launch_g<3, kNW>(grid, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 4: launch_g<4, kNW>(grid, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 1: launch_g<1, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 2: launch_g<2, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 3: launch_g<3, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 4: launch_g<4, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -4;

@@ -11,10 +11,10 @@ namespace ingot {
 // Upper bounds on split counts; they size the workspace.
 constexpr uint32_t kMaxDecodeSplits = 32;
 constexpr uint32_t kMaxPrefillSplits = 16;
-// Completion counters: one per KV head, each on its own 256-byte line (no false sharing of
-// the device-scope atomics between KV heads).
+// Completion counters: one per query head, each on its own 256-byte line (no false sharing of
+// the device-scope atomics between heads).
 constexpr uint32_t kCounterStride = 64;  // uint32 words
-constexpr size_t kCounterBytes = 65536;  // up to 256 KV heads
+constexpr size_t kCounterBytes = 65536;  // up to 256 heads
 
 uint32_t decode_splits(uint32_t n_keys, uint32_t n_head_kv, uint32_t requested);
 uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t requested);
