@@ -36,6 +36,7 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
 # factors from the copy probe (profiles/attn_decode_C3_traffic.md).
 C3_TRAFFIC_BYTES = int((8510.4 * 2.0 + 1652.2) * 1024)
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 MFMA, 2.5 PFLOP/s
+WARMUP_SECONDS = 0.3
 METRIC = "decode-attn HBM GB/s + prefill-attn TFLOPS, Llama-3.2-3B GQA, 1 MI355X"
 
 # name -> (kind, n_keys, pos, n_tok, kv_scale, seed)
@@ -117,9 +118,17 @@ def time_steps(torch, fn, steps, warmup, use_graph):
         with torch.cuda.graph(graph):
             fn()
         run = graph.replay
+    # Warm up for at least `warmup` replays and at least WARMUP_SECONDS of GPU work: the first
+    # tenths of a second after a burst starts run measurably slower (clock ramp, first-touch
+    # translation misses), by up to 15% for the longest prefill.
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < WARMUP_SECONDS:
+        for _ in range(max(1, warmup)):
+            run()
+        torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record(stream)
     for _ in range(steps):

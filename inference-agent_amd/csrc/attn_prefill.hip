@@ -99,12 +99,15 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     const _Float16* Vg = V + size_t(kvh) * kHeadDim;
 
     // Tile copy HBM -> LDS: 32 buffer_load ... lds instructions of 1 KB (4 rows) per tile,
-    // spread over the waves. Lane l of an instruction fills physical chunk l%16 of row
-    // 4*i + l/16, so it fetches the logical chunk (l%16) ^ swizzle(row). The per-lane byte
-    // offsets do not change from tile to tile; the buffer resource is rebased per tile and its
-    // size covers only the visible rows, so rows past kend read as zeros (finite; those keys
-    // are masked, so their P is exactly 0) with no clamping arithmetic.
+    // spread over the waves of the key group and issued in four parts between the compute
+    // phases of the current tile, so that the CU's address unit never receives all of them at
+    // once (a burst stalls every wave at the issue). Lane l of an instruction fills physical
+    // chunk l%16 of row 4*i + l/16, so it fetches the logical chunk (l%16) ^ swizzle(row). The
+    // per-lane byte offsets do not change from tile to tile; the buffer resource is rebased per
+    // tile and its size covers only the visible rows, so rows past kend read as zeros (finite;
+    // those keys are masked, so their P is exactly 0) with no clamping arithmetic.
     constexpr int kInstPerWave = 32 / QW;  // each key group copies its own tiles
+    constexpr int kInstPerPart = kInstPerWave / 4;
     const uint32_t row_bytes = uint32_t(kv_dim) * 2;
     uint32_t dma_off[kInstPerWave];
 #pragma unroll
@@ -115,7 +118,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         const int logical = (lane & 15) ^ (isv ? swz_v(row) : swz_k(row));
         dma_off[k] = uint32_t(row) * row_bytes + 16u * uint32_t(logical);
     }
-    auto issue_tile = [&](uint32_t t, int buf) {
+    auto issue_part = [&](uint32_t t, int buf, int part_) {
         const uint32_t kb = t * kBN;
         char* stage = smem + (kg * 2 + buf) * kStageBytes;
         const uint32_t nrec = min(kend - kb, uint32_t(kBN)) * row_bytes;
@@ -124,7 +127,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<_Float16*>(Vg + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
 #pragma unroll
-        for (int k = 0; k < kInstPerWave; k++) {
+        for (int k = part_ * kInstPerPart; k < (part_ + 1) * kInstPerPart; k++) {
             const int i = qw + k * QW;  // wave-uniform
             const int isv = i >> 4;
             char* dst = stage + isv * kTileBytes + (4 * (i & 15)) * kRowBytes;
@@ -132,23 +135,50 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         }
     };
 
+    // The first tile's copy goes out before anything else, so its latency overlaps the Q load.
+    uint32_t t_first = t_begin + kg;
+    if (t_begin < t_end && t_first < t_end)
+#pragma unroll
+        for (int p = 0; p < 4; p++) issue_part(t_first, 0, p);
+
+    // Q is loaded once per workgroup: every thread converts part of the workgroup's
+    // QW*16 queries x G heads (times scale*log2(e), to f16) into the second stage of each key
+    // group, which the first tile's copy does not touch: queries 0..31 in key group 0's, 32..63
+    // in key group 1's, as rows [query][head][128 dims] with the 16-byte chunk c of a row stored
+    // at c ^ (query & 15), so that the B-operand reads below are bank-conflict free.
+    static_assert(QW * 16 == 64 && G * 32 * 256 <= kStageBytes, "Q staging fits the free stages");
+    {
+        constexpr int kF4 = QW * 16 * G * 32;  // float4 chunks of the workgroup's Q
+        constexpr int NT = 64 * QW * KG;
+#pragma unroll
+        for (int it = 0; it < (kF4 + NT - 1) / NT; it++) {
+            const int idx = tid + it * NT;
+            if (kF4 % NT != 0 && idx >= kF4) break;
+            const int ql = idx / (G * 32), rem = idx % (G * 32);
+            const int h = rem >> 5, c4 = rem & 31;
+            const uint32_t row = min(qblk0 + ql, n_tok - 1);
+            const float4v x = *reinterpret_cast<const float4v*>(
+                q + size_t(row) * q_stride + (size_t(kvh) * G + h) * kHeadDim + 4 * c4);
+            half4 y;
+#pragma unroll
+            for (int e = 0; e < 4; e++) y[e] = _Float16(x[e] * qscale);
+            char* qs = smem + ((ql >> 5) * 2 + 1) * kStageBytes;
+            const int chunk = (c4 >> 1) ^ (ql & 15);
+            *reinterpret_cast<half4*>(qs + ((ql & 31) * G + h) * kRowBytes + 16 * chunk + 8 * (c4 & 1)) = y;
+        }
+    }
+    __syncthreads();
     // B operand Q^T per head: lane holds Q[q0 + li][32*ks + 8*g + e] * scale*log2(e), as f16.
     half8 qb[G][4];
     {
-        const uint32_t row = min(q0 + li, n_tok - 1);
+        const int ql = 16 * qw + li;
+        const char* qs = smem + ((ql >> 5) * 2 + 1) * kStageBytes + (ql & 31) * G * kRowBytes;
 #pragma unroll
         for (int h = 0; h < G; h++)
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++) {
-                const float4v* src = reinterpret_cast<const float4v*>(
-                    q + size_t(row) * q_stride + (size_t(kvh) * G + h) * kHeadDim + 32 * ks + 8 * g);
-                const float4v a = src[0], b = src[1];
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    qb[h][ks][e] = _Float16(a[e] * qscale);
-                    qb[h][ks][4 + e] = _Float16(b[e] * qscale);
-                }
-            }
+            for (int ks = 0; ks < 4; ks++)
+                qb[h][ks] = *reinterpret_cast<const lds_half8*>(
+                    (const lds_void*)(qs + h * kRowBytes + 16 * ((4 * ks + g) ^ (ql & 15))));
     }
 
     // Online-softmax state per head: reference max m (base 2), lane-partial row sum l, O^T.
@@ -171,9 +201,13 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         for (int d = 0; d < 8; d++) O[h][d] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    auto compute_tile = [&](uint32_t t, int buf) {
+    // `dma(p)` issues part p of the next tile's copy.
+    auto compute_tile = [&](uint32_t t, int buf, auto&& dma) {
         const uint32_t kb = t * kBN;
-        if (kb >= kend_w) return;  // every key of this tile is in this wave's future
+        if (kb >= kend_w) {  // every key of this tile is in this wave's future
+            dma(0); dma(1); dma(2); dma(3);
+            return;
+        }
         const char* Ks = smem + (kg * 2 + buf) * kStageBytes;
         const char* Vs = Ks + kTileBytes;
 
@@ -284,13 +318,19 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             }
         };
 
+        dma(0);
         scores(0);
+        dma(1);
         softmax(0);
         pv(0, P);
+        dma(2);
         if (kb + 32 < kend_w) {
             scores(1);
+            dma(3);
             softmax(1);
             pv(1, P);
+        } else {
+            dma(3);
         }
     };
 
@@ -298,14 +338,19 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // (one barrier per step).
     if (t_begin < t_end) {
         const uint32_t steps = (t_end - t_begin + KG - 1) / KG;
-        uint32_t t = t_begin + kg;
-        if (t < t_end) issue_tile(t, 0);
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        uint32_t t = t_first;
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's Q reads and first-tile copies are done
+        __syncthreads();                // ... and everyone's: the Q staging may be overwritten
         int buf = 0;
         for (uint32_t st = 0; st < steps; st++, t += KG) {
-            if (t + KG < t_end) issue_tile(t + KG, buf ^ 1);
-            if (t < t_end) compute_tile(t, buf);
+            const bool next = t + KG < t_end;
+            auto dma = [&](int p) {
+                if (next) issue_part(t + KG, buf ^ 1, p);
+            };
+            if (t < t_end) compute_tile(t, buf, dma);
+            else {
+                dma(0); dma(1); dma(2); dma(3);
+            }
             __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of the next tile have landed
             __syncthreads();                // ... and everyone's; this tile is no longer read
             buf ^= 1;
