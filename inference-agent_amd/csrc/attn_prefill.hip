@@ -421,30 +421,44 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     }
 }
 
-// out[tok][h][d] = sum_s o_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M); 0 if the sum is 0.
-// One 64-thread block per (token, head); thread t owns dims 2t, 2t+1.
-__global__ __launch_bounds__(64) void attn_prefill_combine(const float* __restrict__ part,
-                                                           float* __restrict__ out, uint32_t n_tok,
-                                                           uint32_t n_head, uint32_t q_stride,
-                                                           uint32_t n_splits) {
-    const uint32_t row = blockIdx.x / n_head, h = blockIdx.x % n_head;
-    const int d = threadIdx.x * 2;
+// out[tok][h][d] = sum_s o_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M); 0 if the sum is 0 — the
+// log-sum-exp merge of attn_combine (shaders/kernels.metal:501-516) over the split records.
+// 32 threads per (token, head) record, each owning 4 dims; the loads of 4 splits are in flight
+// at once and folded in online (clamped indices keep them unconditional, masked entries get
+// weight 0).
+constexpr int kCombineThreads = 256;
+__global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
+    const float* __restrict__ part, float* __restrict__ out, uint32_t n_tok, uint32_t n_head,
+    uint32_t q_stride, uint32_t n_splits) {
+    const uint32_t rec = blockIdx.x * (kCombineThreads / 32) + threadIdx.x / 32;
+    if (rec >= n_tok * n_head) return;
+    const uint32_t row = rec / n_head, h = rec % n_head;
+    const int d = 4 * (threadIdx.x % 32);
     const size_t sstride = size_t(n_tok) * n_head * kPartStride;
-    const float* src = part + (size_t(row) * n_head + h) * kPartStride;
-    float M = kNoMax;
-    for (uint32_t s = 0; s < n_splits; s++) M = fmaxf(M, src[s * sstride + 128]);
-    float L = 0.f, O0 = 0.f, O1 = 0.f;
-    for (uint32_t s = 0; s < n_splits; s++) {
-        const float* ps = src + s * sstride;
-        const float wt = fast_exp2(ps[128] - M);
-        L += ps[129] * wt;
-        O0 += ps[d] * wt;
-        O1 += ps[d + 1] * wt;
+    const float* src = part + size_t(rec) * kPartStride;
+    float M = kNoMax, L = 0.f;
+    float4v O = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t s0 = 0; s0 < n_splits; s0 += 4) {
+        float ms[4], ls[4];
+        float4v os[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float* ps = src + min(s0 + u, n_splits - 1) * sstride;
+            ms[u] = s0 + u < n_splits ? ps[128] : kNoMax;
+            ls[u] = ps[129];
+            os[u] = *reinterpret_cast<const float4v*>(ps + d);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const float Mn = fmaxf(M, ms[u]);
+            const float a0 = fast_exp2(M - Mn), a1 = fast_exp2(ms[u] - Mn);
+            L = L * a0 + ls[u] * a1;
+            O = O * a0 + os[u] * a1;
+            M = Mn;
+        }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    float* dst = out + size_t(row) * q_stride + size_t(h) * kHeadDim + d;
-    dst[0] = O0 * inv;
-    dst[1] = O1 * inv;
+    *reinterpret_cast<float4v*>(out + size_t(row) * q_stride + size_t(h) * kHeadDim + d) = O * inv;
 }
 
 constexpr int kQW = 4;  // query waves per workgroup (16 queries x G heads each)
@@ -465,7 +479,9 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
     if (hipGetLastError() != hipSuccess) return -4;
     if (n_splits > 1) {
         const uint32_t n_head = n_head_kv * G;
-        hipLaunchKernelGGL(attn_prefill_combine, dim3(n_tok * n_head), dim3(64), 0, stream, part,
+        const uint32_t per_block = kCombineThreads / 32;
+        hipLaunchKernelGGL(attn_prefill_combine, dim3((n_tok * n_head + per_block - 1) / per_block),
+                           dim3(kCombineThreads), 0, stream, part,
                            out, n_tok, n_head, q_stride, n_splits);
         if (hipGetLastError() != hipSuccess) return -4;
     }
