@@ -26,8 +26,9 @@
  *     stream.
  *
  * Supported shapes: head_dim == 128 and n_head / n_head_kv in {1, 2, 3, 4} — the same
- * envelope as the reference's flash kernels (src/metal_backend.mm:339, 360). Llama-3.2-3B is
- * 24 Q heads / 8 KV heads (group 3).
+ * envelope as the reference's flash kernels (src/metal_backend.mm:339, 360) — and at most 256
+ * query heads (one completion counter each in the workspace). Llama-3.2-3B is 24 Q heads /
+ * 8 KV heads (group 3).
  */
 #ifndef INGOT_ATTN_H
 #define INGOT_ATTN_H
@@ -41,7 +42,7 @@ extern "C" {
 
 #define INGOT_ATTN_OK 0
 #define INGOT_ATTN_EINVAL (-1)      /* null pointer, zero size, pos/n out of range */
-#define INGOT_ATTN_EUNSUPPORTED (-2) /* head_dim != 128 or group size outside 1..4 */
+#define INGOT_ATTN_EUNSUPPORTED (-2) /* head_dim != 128, group size outside 1..4, n_head > 256 */
 #define INGOT_ATTN_EWORKSPACE (-3)  /* workspace smaller than *_workspace_size() */
 #define INGOT_ATTN_EHIP (-4)        /* a HIP runtime call or launch failed */
 

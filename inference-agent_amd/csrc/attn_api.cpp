@@ -121,7 +121,7 @@ const char* ingot_attn_strerror(int code) {
     switch (code) {
         case INGOT_ATTN_OK: return "ok";
         case INGOT_ATTN_EINVAL: return "invalid argument (null/misaligned pointer, zero size or position out of range)";
-        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (head_dim must be 128, n_head/n_head_kv in 1..4)";
+        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (head_dim must be 128, n_head/n_head_kv in 1..4, n_head <= 256)";
         case INGOT_ATTN_EWORKSPACE: return "workspace smaller than the *_workspace_size() figure";
         case INGOT_ATTN_EHIP: return "HIP launch failed";
         default: return "unknown error";
