@@ -17,8 +17,9 @@ rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy kernel of known size
 (profiles/attn_decode_C3_traffic.md).
 
 The same line carries the prefill figures (C4, C5-prefill, C2: TFLOPS and fractions of the
-f16-MFMA and HBM peaks), the decode sweep (C1, C5 lengths) and the CPU baseline (the oracle, a
-C++ restatement of Ingot's CPU attention, on the host cores).
+f16-MFMA and HBM peaks), the decode sweep (C1, C5 lengths), the fused RoPE + KV-cache store
+that precedes attention (GB/s for a 512-token chunk and one decode token) and the CPU baseline
+(the oracle, a C++ restatement of Ingot's CPU attention, on the host cores).
 """
 from __future__ import annotations
 
@@ -44,6 +45,8 @@ DECODE = {"c3": ("C3-decode-4096", 4096, 0.5, 3), "c1": ("C1-decode-512", 512, 1
           "c5d1k": ("C5-decode-1024", 1024, 1.0, 50), "c5d2k": ("C5-decode-2048", 2048, 1.0, 51),
           "c5d8k": ("C5-decode-8192", 8192, 1.0, 53)}
 PREFILL = {"c4": "C4-prefill-512@3584", "c5p": "C5-prefill-2048@6144", "c2": "C2-prefill-512@0"}
+# name -> (pos, n_tok): the KV-store step before attention, for a prefill chunk and a decode token
+KVSTORE = {"kv512": ("kv-store-512@3584", 3584, 512), "kv1": ("kv-store-1@4095", 4095, 1)}
 
 
 def parse():
@@ -52,7 +55,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    help="all | decode | prefill | one of " + ", ".join(list(DECODE) + list(PREFILL)))
+                    help="all | decode | prefill | kvstore | one of " + ", ".join(list(DECODE) + list(PREFILL) + list(KVSTORE)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -88,23 +91,58 @@ class DecodeBench:
 
 
 class PrefillBench:
-    def __init__(self, torch, ia, W, w, seed):
+    """28-layer f16 cache at n_ctx = pos + n_tok; one prefill call per layer per step (the
+    layers' K/V differ, q and out are reused)."""
+
+    def __init__(self, torch, ia, W, w, seed, n_layer=28):
         dev = torch.device("cuda:0")
         g = torch.Generator(device=dev)
         g.manual_seed(seed)
         kv = W.KV_DIM
-        self.w = w
-        self.k = torch.randn(w.n_keys, kv, generator=g, device=dev).half()
-        self.v = torch.randn(w.n_keys, kv, generator=g, device=dev).half()
+        self.w, self.n_layer = w, n_layer
+        self.k = torch.randn(n_layer * w.n_keys, kv, generator=g, device=dev).half()
+        self.v = torch.randn(n_layer * w.n_keys, kv, generator=g, device=dev).half()
         self.q = torch.randn(w.n_tok, W.N_HEAD * W.HEAD_DIM, generator=g, device=dev)
         self.out = torch.empty_like(self.q)
-        self.desc = ia.prefill_desc(W.N_HEAD, W.N_HEAD_KV, W.HEAD_DIM, w.pos, w.n_tok)
+        self.descs = [ia.prefill_desc(W.N_HEAD, W.N_HEAD_KV, W.HEAD_DIM, w.pos, w.n_tok,
+                                      kv_offset=l * w.n_keys * kv) for l in range(n_layer)]
         self.ws = ia.Workspace(dev)
         self.ia = ia
-        self.splits = ia.prefill_splits(self.desc)
+        self.splits = ia.prefill_splits(self.descs[0])
 
     def step(self):
-        self.ia.attn_prefill(self.q, self.k, self.v, self.out, self.desc, workspace=self.ws)
+        for d in self.descs:
+            self.ia.attn_prefill(self.q, self.k, self.v, self.out, d, workspace=self.ws)
+
+
+class KvStoreBench:
+    """ingot_rope_kv_store on n_tok tokens at `pos` for each of 28 layers per step (q rotated in
+    place, K/V into the layer's slice of a 28-layer cache); algorithmic bytes per token: q read
+    and written (f32), k and v read (f32), K and V written (f16) = 36,864 B for 24 Q / 8 KV
+    heads."""
+
+    def __init__(self, torch, ia, W, pos, n_tok, seed, n_layer=28):
+        dev = torch.device("cuda:0")
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        kv = W.KV_DIM
+        n_ctx = pos + n_tok
+        self.n_layer = n_layer
+        self.q = torch.randn(n_tok, W.N_HEAD * W.HEAD_DIM, generator=g, device=dev)
+        self.k = torch.randn(n_tok, kv, generator=g, device=dev)
+        self.v = torch.randn(n_tok, kv, generator=g, device=dev)
+        self.kc = torch.zeros(n_layer * n_ctx, kv, dtype=torch.float16, device=dev)
+        self.vc = torch.zeros_like(self.kc)
+        i = torch.arange(W.HEAD_DIM // 2, device=dev, dtype=torch.float32)
+        self.inv = torch.pow(torch.tensor(500000.0, device=dev), -2.0 * i / W.HEAD_DIM)
+        self.descs = [ia.rope_kv_desc(W.N_HEAD, W.N_HEAD_KV, W.HEAD_DIM, pos, n_tok,
+                                      dst_offset=(l * n_ctx + pos) * kv) for l in range(n_layer)]
+        self.ia = ia
+        self.nbytes = n_tok * (2 * 4 * W.N_HEAD * W.HEAD_DIM + 2 * 4 * kv + 2 * 2 * kv)
+
+    def step(self):
+        for d in self.descs:
+            self.ia.rope_kv_store(self.q, self.k, self.v, self.kc, self.vc, self.inv, d)
 
 
 def time_steps(torch, fn, steps, warmup, use_graph):
@@ -177,7 +215,7 @@ def main():
     use_graph = not args.no_graph
     sel = args.only
     want = lambda key, group: sel in ("all", group, key)
-    res = {"decode": {}, "prefill": {}}
+    res = {"decode": {}, "prefill": {}, "kv_store": {}}
 
     head = None
     for key, (name, n_keys, kv_scale, seed) in DECODE.items():
@@ -202,8 +240,8 @@ def main():
             continue
         w = W.BY_NAME[name]
         b = PrefillBench(torch, ia, W, w, w.seed)
-        steps = max(5, args.steps // 2)
-        sps = time_steps(torch, b.step, steps, args.warmup, use_graph)
+        steps = max(5, args.steps // 5)
+        sps = time_steps(torch, b.step, steps, args.warmup, use_graph) / b.n_layer
         tfs = w.prefill_flops() / sps / 1e12
         gbs = w.prefill_bytes() / sps / 1e9
         res["prefill"][name] = {"us_per_call": round(sps * 1e6, 2), "TFLOPS": round(tfs, 1),
@@ -211,12 +249,27 @@ def main():
                                 "GB/s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
                                 "flops_per_call": w.prefill_flops(), "splits": b.splits}
         if phead is None:
-            phead = (name, sps, tfs, steps)
+            phead = (name, sps, tfs, steps, sps * b.n_layer)
+        del b
+        torch.cuda.empty_cache()
+
+    for key, (name, pos, n_tok) in KVSTORE.items():
+        if not want(key, "kvstore"):
+            continue
+        b = KvStoreBench(torch, ia, W, pos, n_tok, 7)
+        steps = max(5, args.steps // 5)
+        sps = time_steps(torch, b.step, steps, args.warmup, use_graph) / b.n_layer
+        gbs = b.nbytes / sps / 1e9
+        res["kv_store"][name] = {"us_per_call": round(sps * 1e6, 3), "GB/s": round(gbs, 1),
+                                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": b.nbytes}
         del b
         torch.cuda.empty_cache()
 
     cpu = None if args.no_cpu else cpu_baseline(W, args.cpu_seconds)
 
+    if head is None and phead is None:
+        print(json.dumps({"metric": METRIC, "results": res}), flush=True)
+        return
     if head is not None:
         sps, us_thru, nbytes, gbs, steps = head
         value, unit, ms = gbs, "GB/s", sps * 1e3
@@ -227,12 +280,12 @@ def main():
         workload = ("C3 decode attention, KV 4096, 24 Q / 8 KV heads, hd 128, f16 cache, "
                     "28-layer slice rotation (470 MB)")
     else:
-        name, sps, tfs, steps = phead
-        value, unit, ms = tfs, "TFLOPS", sps * 1e3
+        name, sps, tfs, steps, step_s = phead
+        value, unit, ms = tfs, "TFLOPS", step_s * 1e3
         roofline = {"bound": "mfma", "achieved": round(tfs, 1), "peak": MFMA_F16_PEAK_TFS,
                     "unit": "TFLOP/s", "frac": round(tfs / MFMA_F16_PEAK_TFS, 4), "traffic": None,
                     "kernel": "attn_prefill_kernel<3,4>"}
-        workload = f"{name} causal prefill, 24 Q / 8 KV heads, hd 128, f16 cache"
+        workload = f"{name} causal prefill, 24 Q / 8 KV heads, hd 128, f16 cache, 28 layers"
     line = {
         "metric": METRIC, "value": round(value, 2), "unit": unit, "n_gpus": 1, "steps": steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,

@@ -7,7 +7,8 @@
  *       decode  (n_tok == 1): attn_decode_g3 + attn_combine (shaders/kernels.metal:428-516)
  *       prefill (n_tok  > 1): attn_prefill                  (shaders/kernels.metal:518-633)
  *   - `encode_kv_store` (src/metal_backend.mm:395-409), the writer of the f16 KV cache
- *       (rope_k_to_cache + to_half, shaders/kernels.metal:270-282, 779-782).
+ *       (rope_k_to_cache + to_half, shaders/kernels.metal:270-282, 779-782), together with the
+ *       rope on q before it (src/metal_backend.mm:443): ingot_rope_kv_store.
  * The numerics follow Ingot's CPU attention (src/cpu_backend.cpp:46-69, src/ops.cpp:234-241)
  * on K/V rounded to f16 (round-to-nearest-even).
  *
@@ -76,6 +77,22 @@ typedef struct IngotAttnPrefillDesc {
     float scale;
 } IngotAttnPrefillDesc;
 
+/* KV-store descriptor. Mirrors RopeKParams (src/metal_backend.mm:31: n_heads, head_dim, pos,
+ * dst_offset, row_stride) plus what the fused launch also covers: the query heads rotated in
+ * place (the reference's separate `rope` dispatch on q, src/metal_backend.mm:443) and the token
+ * count. dst_offset is the cache element offset of token 0's row,
+ * (layer*n_ctx + pos) * n_head_kv*head_dim (`slot`, src/metal_backend.mm:437). */
+typedef struct IngotRopeKvDesc {
+    uint32_t n_head;     /* query heads (used when q != NULL) */
+    uint32_t n_head_kv;
+    uint32_t head_dim;   /* even; a multiple of 4 here */
+    uint32_t pos;        /* position of token 0 */
+    uint32_t n_tok;
+    uint64_t dst_offset;
+    uint32_t q_stride;   /* elements between q rows, >= n_head*head_dim */
+    uint32_t kv_stride;  /* elements between k (and v) rows, >= n_head_kv*head_dim */
+} IngotRopeKvDesc;
+
 /* Bytes of device workspace the call with this descriptor needs. The workspace must be
  * zero-filled once when it is allocated (it holds completion counters that every call leaves
  * at zero again). One workspace of the largest size serves every smaller call. Returns 0 for an
@@ -107,6 +124,19 @@ int ingot_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
 int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
                        void* workspace, size_t workspace_bytes, const IngotAttnPrefillDesc* d,
                        void* stream);
+
+/* RoPE and KV-cache store for n_tok tokens at positions pos..pos+n_tok-1, in one launch:
+ *   q        [n_tok][q_stride] f32, rotated in place (NULL: only K and V are handled)
+ *   k, v     [n_tok][kv_stride] f32 projections
+ *   k_cache, v_cache: f16 cache bases; rows dst_offset/kv_dim .. + n_tok-1 are written
+ *   inv_freq [head_dim/2] f32 rotary frequencies (Model::rope_inv_freq, src/model.cpp:59-68)
+ * Pair (2i, 2i+1) of each q/k head is rotated by angle float(pos + t) * inv_freq[i]
+ * (ops::rope, src/ops.cpp:243-255); K and V are rounded to f16, round to nearest even.
+ * Replaces encode_rope on q plus encode_kv_store (src/metal_backend.mm:395-409, 443-444) and
+ * does what src/cpu_backend.cpp:43-49 does per token. No workspace. */
+int ingot_rope_kv_store(float* q, const float* k, const float* v, uint16_t* k_cache,
+                        uint16_t* v_cache, const float* inv_freq, const IngotRopeKvDesc* d,
+                        void* stream);
 
 /* Static description of an error code (never NULL). */
 const char* ingot_attn_strerror(int code);

@@ -117,6 +117,29 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
 }
 
+int ingot_rope_kv_store(float* q, const float* k, const float* v, uint16_t* k_cache,
+                        uint16_t* v_cache, const float* inv_freq, const IngotRopeKvDesc* d,
+                        void* stream) {
+    if (!d || !k || !v || !k_cache || !v_cache || !inv_freq) return INGOT_ATTN_EINVAL;
+    if (d->n_head_kv == 0 || d->head_dim == 0 || d->n_tok == 0) return INGOT_ATTN_EINVAL;
+    if (d->head_dim % 4 != 0) return INGOT_ATTN_EUNSUPPORTED;
+    const uint64_t kv_dim = uint64_t(d->n_head_kv) * d->head_dim;
+    if (d->kv_stride < kv_dim || d->kv_stride % 4 != 0) return INGOT_ATTN_EINVAL;
+    if (d->dst_offset % 4 != 0) return INGOT_ATTN_EINVAL;
+    if (uint64_t(d->pos) + d->n_tok > 0xffffffffull) return INGOT_ATTN_EINVAL;
+    if (q && (d->n_head == 0 || d->q_stride < uint64_t(d->n_head) * d->head_dim || d->q_stride % 4 != 0 || !aligned16(q)))
+        return INGOT_ATTN_EINVAL;
+    if (!aligned16(k) || !aligned16(v) || (reinterpret_cast<uintptr_t>(k_cache) & 7u) != 0 ||
+        (reinterpret_cast<uintptr_t>(v_cache) & 7u) != 0)
+        return INGOT_ATTN_EINVAL;
+    auto* kc = reinterpret_cast<_Float16*>(k_cache) + d->dst_offset;
+    auto* vc = reinterpret_cast<_Float16*>(v_cache) + d->dst_offset;
+    const int lrc = ingot::launch_rope_kv_store(q, k, v, kc, vc, inv_freq, d->n_head, d->n_head_kv,
+                                                d->head_dim, d->pos, d->n_tok, d->q_stride,
+                                                d->kv_stride, static_cast<hipStream_t>(stream));
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
+}
+
 const char* ingot_attn_strerror(int code) {
     switch (code) {
         case INGOT_ATTN_OK: return "ok";

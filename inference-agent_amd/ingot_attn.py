@@ -24,6 +24,7 @@ EXPORTS = (
     "ingot_attn_prefill_splits",
     "ingot_attn_decode",
     "ingot_attn_prefill",
+    "ingot_rope_kv_store",
     "ingot_attn_strerror",
     "ingot_attn_version",
 )
@@ -59,6 +60,21 @@ class PrefillDesc(ctypes.Structure):
     ]
 
 
+class RopeKvDesc(ctypes.Structure):
+    """IngotRopeKvDesc; mirrors RopeKParams (src/metal_backend.mm:31) plus q heads and n_tok."""
+
+    _fields_ = [
+        ("n_head", c_uint32),
+        ("n_head_kv", c_uint32),
+        ("head_dim", c_uint32),
+        ("pos", c_uint32),
+        ("n_tok", c_uint32),
+        ("dst_offset", c_uint64),
+        ("q_stride", c_uint32),
+        ("kv_stride", c_uint32),
+    ]
+
+
 _lib = None
 
 
@@ -86,6 +102,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ingot_attn_decode.restype = c_int
     lib.ingot_attn_prefill.argtypes = [c_void_p] * 5 + [c_size_t, PP, c_void_p]
     lib.ingot_attn_prefill.restype = c_int
+    lib.ingot_rope_kv_store.argtypes = [c_void_p] * 6 + [ctypes.POINTER(RopeKvDesc), c_void_p]
+    lib.ingot_rope_kv_store.restype = c_int
     lib.ingot_attn_strerror.argtypes = [c_int]
     lib.ingot_attn_strerror.restype = ctypes.c_char_p
     lib.ingot_attn_version.argtypes = []
@@ -104,6 +122,13 @@ def prefill_desc(n_head, n_head_kv, head_dim, pos, n_tok, kv_offset=0, q_stride=
     scale = 1.0 / math.sqrt(head_dim) if scale is None else scale
     q_stride = n_head * head_dim if q_stride is None else q_stride
     return PrefillDesc(n_head, n_head_kv, head_dim, pos, n_tok, kv_offset, q_stride, n_splits, scale)
+
+
+def rope_kv_desc(n_head, n_head_kv, head_dim, pos, n_tok, dst_offset=0, q_stride=None,
+                 kv_stride=None):
+    q_stride = n_head * head_dim if q_stride is None else q_stride
+    kv_stride = n_head_kv * head_dim if kv_stride is None else kv_stride
+    return RopeKvDesc(n_head, n_head_kv, head_dim, pos, n_tok, dst_offset, q_stride, kv_stride)
 
 
 def _check(rc: int, what: str) -> None:
@@ -189,3 +214,17 @@ def decode_splits(desc: DecodeDesc) -> int:
 
 def prefill_splits(desc: PrefillDesc) -> int:
     return int(load_library().ingot_attn_prefill_splits(ctypes.byref(desc)))
+
+
+def rope_kv_store(q, k, v, k_cache, v_cache, inv_freq, desc: RopeKvDesc, stream=None):
+    """RoPE on q (in place; None to skip) and k, K and V into the f16 cache rows, one launch.
+
+    q, k, v, inv_freq: f32 CUDA tensors; k_cache, v_cache: f16 (or 16-bit views) CUDA tensors.
+    Replaces the reference's rope + rope_k_to_cache + to_half (src/metal_backend.mm:395-409).
+    """
+    lib = load_library()
+    rc = lib.ingot_rope_kv_store(
+        None if q is None else c_void_p(q.data_ptr()), c_void_p(k.data_ptr()),
+        c_void_p(v.data_ptr()), c_void_p(k_cache.data_ptr()), c_void_p(v_cache.data_ptr()),
+        c_void_p(inv_freq.data_ptr()), ctypes.byref(desc), _stream_ptr(stream))
+    _check(rc, "ingot_rope_kv_store")

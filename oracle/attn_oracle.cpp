@@ -17,7 +17,14 @@
 //   - the f16 KV cache of the Metal backend (src/metal_backend.mm:197-198, 437) written with
 //     half(x) (shaders/kernels.metal:280-281, 781): round-to-nearest-even binary16. The
 //     reference CPU cache is f32 (src/cpu_backend.h:23); here it holds the same f16-rounded
-//     values widened to f32, so the CPU and GPU paths see identical K/V.
+//     values widened to f32, so the CPU and GPU paths see identical K/V;
+//   - the step before attention: ops::rope, src/ops.cpp:243-255 (pairs (2i, 2i+1) of each head
+//     rotated by angle float(pos) * inv_freq[i], cosf/sinf), applied to q and k
+//     (src/cpu_backend.cpp:43-44), then K and V copied into the cache row of pos
+//     (src/cpu_backend.cpp:46-49); in the f16 cache this is rope_k_to_cache + to_half
+//     (shaders/kernels.metal:270-282, 779-782; src/metal_backend.mm:395-409);
+//   - the rotary frequencies, src/model.cpp:59-68: an iterated multiply by
+//     theta^(-2/head_dim) starting at 1, each optionally divided by rope_freqs.weight[i].
 //
 // Differences that do not affect results beyond f32 rounding: Apple clang contracts
 // `s += q*k` into an FMA on arm64 (fp-contract=on); this file is built with
@@ -139,9 +146,61 @@ void parallel_for(int n, int n_threads, F&& f) {
     for (auto& t : pool) t.join();
 }
 
+// ops::rope, src/ops.cpp:243-255, on one row at position `pos`.
+void rope_row(float* x, int n_heads, int head_dim, int pos, const float* inv_freq) {
+    const int half = head_dim / 2;
+    for (int h = 0; h < n_heads; h++) {
+        float* v = x + size_t(h) * head_dim;
+        for (int i = 0; i < half; i++) {
+            const float angle = float(pos) * inv_freq[i];
+            const float c = cosf(angle), s = sinf(angle);
+            const float x0 = v[2 * i], x1 = v[2 * i + 1];
+            v[2 * i] = x0 * c - x1 * s;
+            v[2 * i + 1] = x0 * s + x1 * c;
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+void oracle_rope_inv_freq(float theta, int head_dim, const float* factors, float* out) {
+    const float theta_scale = powf(theta, -2.0f / float(head_dim));
+    float freq = 1.0f;
+    for (int i = 0; i < head_dim / 2; i++) {
+        out[i] = factors ? freq / factors[i] : freq;
+        freq *= theta_scale;
+    }
+}
+
+void oracle_rope(float* x, int n_tok, int row_stride, int n_heads, int head_dim, int pos,
+                 const float* inv_freq) {
+    for (int t = 0; t < n_tok; t++) rope_row(x + size_t(t) * row_stride, n_heads, head_dim, pos + t, inv_freq);
+}
+
+int oracle_rope_kv_store(float* q, int q_stride, int n_head, const float* k, const float* v,
+                         int kv_stride, uint16_t* k_cache, uint16_t* v_cache, size_t dst_offset,
+                         int n_head_kv, int head_dim, int pos, int n_tok, const float* inv_freq) {
+    if (!k || !v || !k_cache || !v_cache || !inv_freq || n_head_kv <= 0 || head_dim <= 0 ||
+        head_dim % 2 != 0 || pos < 0 || n_tok <= 0 || kv_stride < n_head_kv * head_dim)
+        return -1;
+    const size_t kv_dim = size_t(n_head_kv) * head_dim;
+    std::vector<float> kr(kv_dim);
+    for (int t = 0; t < n_tok; t++) {
+        if (q) rope_row(q + size_t(t) * q_stride, n_head, head_dim, pos + t, inv_freq);
+        std::memcpy(kr.data(), k + size_t(t) * kv_stride, kv_dim * sizeof(float));
+        rope_row(kr.data(), n_head_kv, head_dim, pos + t, inv_freq);
+        uint16_t* kd = k_cache + dst_offset + size_t(t) * kv_dim;
+        uint16_t* vd = v_cache + dst_offset + size_t(t) * kv_dim;
+        const float* vs = v + size_t(t) * kv_stride;
+        for (size_t i = 0; i < kv_dim; i++) {
+            kd[i] = float_to_half(kr[i]);
+            vd[i] = float_to_half(vs[i]);
+        }
+    }
+    return 0;
+}
 
 void oracle_f32_to_f16(const float* in, uint16_t* out, size_t n) {
     for (size_t i = 0; i < n; i++) out[i] = float_to_half(in[i]);

@@ -24,6 +24,19 @@ int oracle_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t*
                         int n_head, int n_head_kv, int head_dim, int pos, int n_tok, int q_stride,
                         float scale, int n_threads);
 
+// Rotary frequencies (head_dim/2 entries); factors may be NULL.
+void oracle_rope_inv_freq(float theta, int head_dim, const float* factors, float* out);
+
+// ops::rope in place on x [n_tok][row_stride], token t at position pos + t.
+void oracle_rope(float* x, int n_tok, int row_stride, int n_heads, int head_dim, int pos,
+                 const float* inv_freq);
+
+// RoPE on q (in place; q may be NULL) and k, then K and V rounded to f16 into the cache rows
+// dst_offset + t*kv_dim (kv_dim = n_head_kv*head_dim). Returns 0 or -1.
+int oracle_rope_kv_store(float* q, int q_stride, int n_head, const float* k, const float* v,
+                         int kv_stride, uint16_t* k_cache, uint16_t* v_cache, size_t dst_offset,
+                         int n_head_kv, int head_dim, int pos, int n_tok, const float* inv_freq);
+
 #ifdef __cplusplus
 }
 #endif

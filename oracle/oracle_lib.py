@@ -32,6 +32,11 @@ def lib() -> ctypes.CDLL:
         L.oracle_attn_decode.restype = c_int
         L.oracle_attn_prefill.argtypes = [c_void_p] * 4 + [c_int] * 6 + [c_float, c_int]
         L.oracle_attn_prefill.restype = c_int
+        L.oracle_rope_inv_freq.argtypes = [c_float, c_int, c_void_p, c_void_p]
+        L.oracle_rope.argtypes = [c_void_p] + [c_int] * 5 + [c_void_p]
+        L.oracle_rope_kv_store.argtypes = ([c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p,
+                                            c_void_p, c_size_t] + [c_int] * 4 + [c_void_p])
+        L.oracle_rope_kv_store.restype = c_int
         _lib = L
     return _lib
 
@@ -87,3 +92,38 @@ def attn_prefill(q, k_bits, v_bits, n_head, n_head_kv, head_dim, pos, n_tok, sca
     if rc != 0:
         raise ValueError("oracle_attn_prefill: bad arguments")
     return out
+
+
+def rope_inv_freq(theta: float, head_dim: int, factors=None) -> np.ndarray:
+    """src/model.cpp:59-68: head_dim/2 rotary frequencies."""
+    out = np.empty(head_dim // 2, dtype=np.float32)
+    f = None if factors is None else np.ascontiguousarray(factors, dtype=np.float32)
+    lib().oracle_rope_inv_freq(theta, head_dim, None if f is None else _ptr(f), _ptr(out))
+    return out
+
+
+def rope(x, n_heads, head_dim, pos, inv_freq) -> np.ndarray:
+    """ops::rope (src/ops.cpp:243-255) on rows x [n_tok][row_stride], token t at pos + t."""
+    x = np.array(x, dtype=np.float32, copy=True, order="C")
+    x2 = x.reshape(x.shape[0], -1) if x.ndim > 1 else x.reshape(1, -1)
+    inv_freq = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    lib().oracle_rope(_ptr(x2), x2.shape[0], x2.shape[1], n_heads, head_dim, pos, _ptr(inv_freq))
+    return x
+
+
+def rope_kv_store(q, k, v, k_cache, v_cache, dst_offset, n_head, n_head_kv, head_dim, pos,
+                  inv_freq):
+    """RoPE on q (returned, or None) and k; K, V as f16 into copies of the caches (returned)."""
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    n_tok = k.shape[0]
+    kc = np.array(k_cache, dtype=np.uint16, copy=True, order="C")
+    vc = np.array(v_cache, dtype=np.uint16, copy=True, order="C")
+    qq = None if q is None else np.array(q, dtype=np.float32, copy=True, order="C")
+    inv_freq = np.ascontiguousarray(inv_freq, dtype=np.float32)
+    rc = lib().oracle_rope_kv_store(None if qq is None else _ptr(qq), 0 if qq is None else qq.shape[1],
+                                    n_head, _ptr(k), _ptr(v), k.shape[1], _ptr(kc), _ptr(vc),
+                                    dst_offset, n_head_kv, head_dim, pos, n_tok, _ptr(inv_freq))
+    if rc != 0:
+        raise ValueError("oracle_rope_kv_store: bad arguments")
+    return qq, kc, vc

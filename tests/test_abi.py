@@ -66,6 +66,8 @@ def test_struct_layout_matches_c():
                sizeof(IngotAttnPrefillDesc), offsetof(IngotAttnPrefillDesc, kv_offset));
         printf("%zu %zu\n", offsetof(IngotAttnPrefillDesc, q_stride),
                offsetof(IngotAttnPrefillDesc, scale));
+        printf("%zu %zu %zu %zu\n", sizeof(IngotRopeKvDesc), offsetof(IngotRopeKvDesc, dst_offset),
+               offsetof(IngotRopeKvDesc, q_stride), offsetof(IngotRopeKvDesc, kv_stride));
         return 0;
     }
     """
@@ -75,9 +77,10 @@ def test_struct_layout_matches_c():
         open(c, "w").write(src)
         subprocess.run(["gcc", "-I", INCLUDE, c, "-o", exe], check=True)
         vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True).stdout.split()]
-    D, P = ingot_attn.DecodeDesc, ingot_attn.PrefillDesc
+    D, P, R = ingot_attn.DecodeDesc, ingot_attn.PrefillDesc, ingot_attn.RopeKvDesc
     assert vals == [ctypes.sizeof(D), D.kv_offset.offset, D.scale.offset, ctypes.sizeof(P),
-                    P.kv_offset.offset, P.q_stride.offset, P.scale.offset]
+                    P.kv_offset.offset, P.q_stride.offset, P.scale.offset, ctypes.sizeof(R),
+                    R.dst_offset.offset, R.q_stride.offset, R.kv_stride.offset]
 
 
 def test_host_validation(lib):
@@ -115,3 +118,23 @@ def test_split_resolution(lib):
             assert 1 <= s <= min(n_keys, 1024)
             per = -(-n_keys // s)
             assert (s - 1) * per < n_keys  # no empty split
+
+
+def test_rope_kv_store_validation(lib):
+    """Argument checks of ingot_rope_kv_store run before any HIP call (fake, aligned pointers)."""
+    import ingot_attn as ia
+
+    P = ctypes.c_void_p
+    a = P(1 << 20)  # 16-byte aligned, never dereferenced: every call below is rejected first
+    f = lib.ingot_rope_kv_store
+    ok = ia.rope_kv_desc(24, 8, 128, 0, 4)
+    assert f(a, None, a, a, a, a, ctypes.byref(ok), None) == -1            # k missing
+    assert f(a, a, a, a, a, None, ctypes.byref(ok), None) == -1            # inv_freq missing
+    assert f(a, a, a, a, a, a, None, None) == -1                           # no descriptor
+    assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 126, 0, 4)), None) == -2
+    assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 128, 0, 0)), None) == -1
+    assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 128, 0, 4, kv_stride=1000)), None) == -1
+    assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 128, 0, 4, q_stride=3000)), None) == -1
+    assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 128, 0, 4, dst_offset=2)), None) == -1
+    assert f(a, a, P((1 << 20) + 4), a, a, a, ctypes.byref(ok), None) == -1  # misaligned v
+    assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 128, 0xffffffff, 2)), None) == -1

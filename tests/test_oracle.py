@@ -229,3 +229,66 @@ def test_oracle_rejects_bad_arguments(oracle_mod):
         oracle_mod.attn_decode(q, kb, kb, 24, 7, HD, 4)  # 24 % 7 != 0
     with pytest.raises(ValueError):
         oracle_mod.attn_decode(q, kb, kb, 24, 8, HD, 0)
+
+
+# --- RoPE and the KV store (src/ops.cpp:243-255, src/model.cpp:59-68, src/cpu_backend.cpp:43-49)
+
+
+def test_rope_inv_freq_closed_form(oracle_mod):
+    """inv_freq[i] = theta^(-2i/d) (iterated multiply: drift ~1e-6), divided by the factors."""
+    for theta, d in ((10000.0, 128), (500000.0, 128), (10000.0, 64)):
+        got = oracle_mod.rope_inv_freq(theta, d).astype(np.float64)
+        want = theta ** (-2.0 * np.arange(d // 2) / d)
+        assert got[0] == 1.0
+        np.testing.assert_allclose(got, want, rtol=2e-5)
+    factors = np.linspace(1.0, 8.0, 64).astype(np.float32)
+    base = oracle_mod.rope_inv_freq(500000.0, 128)
+    np.testing.assert_allclose(oracle_mod.rope_inv_freq(500000.0, 128, factors), base / factors, rtol=1e-6)
+
+
+def _rope_f64(x, n_heads, hd, pos, inv_freq):
+    """Textbook rotation of pairs (2i, 2i+1) in float64, by the angle the reference forms in
+    float32: float(pos) * inv_freq[i] (src/ops.cpp:248), rounded once."""
+    x = np.asarray(x, dtype=np.float64).reshape(x.shape[0], n_heads, hd // 2, 2).copy()
+    p32 = (pos + np.arange(x.shape[0])).astype(np.float32)
+    ang = (p32[:, None] * inv_freq.astype(np.float32)[None, :]).astype(np.float64)
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    x0, x1 = x[..., 0].copy(), x[..., 1].copy()
+    x[..., 0] = x0 * c - x1 * s
+    x[..., 1] = x0 * s + x1 * c
+    return x.reshape(x.shape[0], -1)
+
+
+def test_rope_pins(oracle_mod):
+    rng = np.random.default_rng(3)
+    inv = oracle_mod.rope_inv_freq(500000.0, 128)
+    x = rng.standard_normal((6, 3 * 128)).astype(np.float32)
+    # position 0 is the identity (cos 0 = 1, sin 0 = 0 exactly)
+    assert np.array_equal(oracle_mod.rope(x[:1], 3, 128, 0, inv), x[:1])
+    # the textbook rotation of adjacent pairs, in float64 (pins pair layout, sign, angle)
+    for pos in (1, 17, 4000):
+        got = oracle_mod.rope(x, 3, 128, pos, inv)
+        np.testing.assert_allclose(got, _rope_f64(x, 3, 128, pos, inv), rtol=0, atol=2e-6)
+    # a rotation keeps every pair's length
+    got = oracle_mod.rope(x, 3, 128, 123, inv).reshape(6, -1, 2)
+    np.testing.assert_allclose(np.hypot(got[..., 0], got[..., 1]),
+                               np.hypot(*x.reshape(6, -1, 2).transpose(2, 0, 1)), rtol=1e-5)
+
+
+def test_kv_store_is_rope_then_f16(oracle_mod):
+    rng = np.random.default_rng(5)
+    hkv, hd, n_tok, pos, n_ctx = 2, 128, 5, 7, 16
+    inv = oracle_mod.rope_inv_freq(10000.0, hd)
+    k = rng.standard_normal((n_tok, hkv * hd)).astype(np.float32)
+    v = rng.standard_normal((n_tok, hkv * hd)).astype(np.float32)
+    q = rng.standard_normal((n_tok, 4 * hd)).astype(np.float32)
+    canary = np.full((2 * n_ctx, hkv * hd), 0x7E00, dtype=np.uint16)
+    dst = (n_ctx + pos) * hkv * hd  # layer 1
+    qq, kc, vc = oracle_mod.rope_kv_store(q, k, v, canary, canary, dst, 4, hkv, hd, pos, inv)
+    rows = slice(n_ctx + pos, n_ctx + pos + n_tok)
+    assert np.array_equal(vc[rows], oracle_mod.f32_to_f16(v))
+    assert np.array_equal(kc[rows], oracle_mod.f32_to_f16(oracle_mod.rope(k, hkv, hd, pos, inv)))
+    np.testing.assert_array_equal(qq, oracle_mod.rope(q, 4, hd, pos, inv))
+    others = np.ones(2 * n_ctx, dtype=bool)
+    others[rows] = False
+    assert (kc[others] == 0x7E00).all() and (vc[others] == 0x7E00).all()
