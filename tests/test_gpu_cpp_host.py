@@ -1,0 +1,25 @@
+"""The C++ host side (inference-agent_amd/host/ingot_hip_attention.hpp, ingot::HipAttention)
+driven as Ingot's forward_batch drives its attention step: chunked prefill then decode steps on
+one layer of a 2-layer cache, each compared with the CPU oracle (max|d| <= 2e-3, rel-L2 <=
+1e-3), the V cache bits, the untouched layer, and the reference's std::runtime_error behaviour
+on range errors. The checks run inside tests/cpp/test_hip_attention (built by build())."""
+from __future__ import annotations
+
+import os
+import subprocess
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+EXE = os.path.join(ROOT, "tests", "cpp", "test_hip_attention")
+
+
+def test_cpp_host_side():
+    if not os.path.exists(EXE):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp")], check=True)
+    print("[cpp host] running tests/cpp/test_hip_attention", flush=True)
+    r = subprocess.run([EXE], capture_output=True, text=True, timeout=100)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0 and "ALL PASSED" in r.stdout
