@@ -29,6 +29,22 @@ def small(seed, n_head, n_head_kv, pos, n_tok, n_ctx):
     return dict(q=q, k=kb, v=vb, out=out, n_head=n_head, n_head_kv=n_head_kv, pos=pos, n_tok=n_tok)
 
 
+def kv_store(seed, n_head, n_head_kv, pos, n_tok, n_ctx, theta):
+    """RoPE + f16 KV store of n_tok tokens at pos into layer 1 of a 2-layer cache."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    hd = 128
+    inv = oracle_lib.rope_inv_freq(theta, hd)
+    q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    k = rng.standard_normal((n_tok, n_head_kv * hd)).astype(np.float32)
+    v = rng.standard_normal((n_tok, n_head_kv * hd)).astype(np.float32)
+    cache = np.zeros((2 * n_ctx, n_head_kv * hd), dtype=np.uint16)
+    dst = (n_ctx + pos) * n_head_kv * hd
+    q_out, kc, vc = oracle_lib.rope_kv_store(q, k, v, cache, cache, dst, n_head, n_head_kv, hd, pos, inv)
+    rows = slice(n_ctx + pos, n_ctx + pos + n_tok)
+    return dict(q=q, k=k, v=v, inv_freq=inv, q_out=q_out, k_rows=kc[rows], v_rows=vc[rows],
+                n_head=n_head, n_head_kv=n_head_kv, pos=pos, n_tok=n_tok, n_ctx=n_ctx)
+
+
 def main():
     np.savez_compressed(os.path.join(HERE, "small_decode_g3.npz"), **small(101, 6, 2, 69, 1, 70))
     np.savez_compressed(os.path.join(HERE, "small_prefill_g3.npz"), **small(102, 6, 2, 20, 37, 57))
@@ -40,6 +56,7 @@ def main():
         digest = hashlib.sha256(q.tobytes() + kb.tobytes() + vb.tobytes()).hexdigest()
         out = oracle_lib.attn_decode(q, kb, vb, 24, 8, 128, w.n_keys, threads=8)
         np.savez_compressed(os.path.join(HERE, f"{w.name}.npz"), out=out, digest=np.array(digest))
+    np.savez_compressed(os.path.join(HERE, "small_kv_store.npz"), **kv_store(104, 24, 8, 2000, 5, 2048, 500000.0))
     print("written")
 
 

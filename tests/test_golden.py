@@ -74,3 +74,44 @@ def test_gpu_matches_config_fixtures(wname):
                    torch.from_numpy(vb.view(np.int16)).to(dev), out, ia.decode_desc(24, 8, 128, w.n_keys))
     torch.cuda.synchronize()
     assert_parity(out.cpu().numpy(), f["out"], wname)
+
+
+def test_oracle_reproduces_kv_store_fixture(oracle_mod):
+    f = np.load(os.path.join(GOLD, "small_kv_store.npz"))
+    H, HKV, pos, n, n_ctx = (int(f[x]) for x in ("n_head", "n_head_kv", "pos", "n_tok", "n_ctx"))
+    cache = np.zeros((2 * n_ctx, HKV * 128), dtype=np.uint16)
+    q_out, kc, vc = oracle_mod.rope_kv_store(f["q"], f["k"], f["v"], cache, cache,
+                                             (n_ctx + pos) * HKV * 128, H, HKV, 128, pos, f["inv_freq"])
+    rows = slice(n_ctx + pos, n_ctx + pos + n)
+    assert np.array_equal(q_out, f["q_out"])
+    assert np.array_equal(kc[rows], f["k_rows"]) and np.array_equal(vc[rows], f["v_rows"])
+
+
+@pytest.mark.gpu
+def test_gpu_matches_kv_store_fixture():
+    """V rows bit-exact; K rows within 1 f16 step; q within 2e-6 relative (see
+    tests/test_gpu_kv_store.py for why K may differ by one step)."""
+    import torch
+
+    ensure_built("lib")
+    import ingot_attn as ia
+
+    f = np.load(os.path.join(GOLD, "small_kv_store.npz"))
+    H, HKV, pos, n, n_ctx = (int(f[x]) for x in ("n_head", "n_head_kv", "pos", "n_tok", "n_ctx"))
+    print(f"[golden] small_kv_store H={H} HKV={HKV} pos={pos} n_tok={n}", flush=True)
+    dev = torch.device("cuda:0")
+    q = torch.from_numpy(f["q"]).to(dev)
+    kc = torch.zeros(2 * n_ctx, HKV * 128, dtype=torch.int16, device=dev)
+    vc = torch.zeros_like(kc)
+    ia.rope_kv_store(q, torch.from_numpy(f["k"]).to(dev), torch.from_numpy(f["v"]).to(dev), kc, vc,
+                     torch.from_numpy(f["inv_freq"]).to(dev),
+                     ia.rope_kv_desc(H, HKV, 128, pos, n, dst_offset=(n_ctx + pos) * HKV * 128))
+    torch.cuda.synchronize()
+    rows = slice(n_ctx + pos, n_ctx + pos + n)
+    k_got = kc.cpu().numpy().view(np.uint16)[rows].astype(np.int32)
+    v_got = vc.cpu().numpy().view(np.uint16)[rows]
+    assert np.array_equal(v_got, f["v_rows"])
+    key = lambda b: np.where(b & 0x8000, -(b & 0x7FFF), b & 0x7FFF)
+    assert np.abs(key(k_got) - key(f["k_rows"].astype(np.int32))).max() <= 1
+    q_want = f["q_out"]
+    assert (np.abs(q.cpu().numpy() - q_want) <= 2e-6 * (1 + np.abs(q_want))).all()
