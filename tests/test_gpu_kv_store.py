@@ -153,3 +153,28 @@ def test_store_then_attention_end_to_end(dev, oracle_mod):
     ia.attn_decode(qd[-1].contiguous(), kcd, vcd, outd, ia.decode_desc(H, HKV, HD, pos + n_tok))
     torch.cuda.synchronize()
     assert_parity(outd.cpu().numpy(), want[-1], "decode over the stored cache")
+
+
+@pytest.mark.parametrize("n_head,n_head_kv,hd", [(8, 8, 128), (16, 4, 128), (3, 1, 128), (32, 8, 64), (4, 2, 256)])
+def test_rope_kv_store_shapes(dev, oracle_mod, n_head, n_head_kv, hd):
+    """Other head counts and head sizes (the store itself is not limited to head_dim 128)."""
+    import torch
+    import ingot_attn as ia
+
+    print(f"[rope_kv_store shapes] H={n_head} HKV={n_head_kv} hd={hd}", flush=True)
+    rng = np.random.default_rng(n_head * 31 + hd)
+    pos, n_tok, n_ctx = 123, 9, 140
+    kv = n_head_kv * hd
+    inv = oracle_mod.rope_inv_freq(10000.0, hd)
+    q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    k = rng.standard_normal((n_tok, kv)).astype(np.float32)
+    v = rng.standard_normal((n_tok, kv)).astype(np.float32)
+    cache = np.full((n_ctx, kv), 0x7E00, dtype=np.uint16)
+    q_w, kc_w, vc_w = oracle_mod.rope_kv_store(q, k, v, cache, cache, pos * kv, n_head, n_head_kv, hd, pos, inv)
+    qd = _t(q, dev)
+    kcd, vcd = _t(cache.view(np.int16), dev), _t(cache.view(np.int16), dev)
+    ia.rope_kv_store(qd, _t(k, dev), _t(v, dev), kcd, vcd, _t(inv, dev),
+                     ia.rope_kv_desc(n_head, n_head_kv, hd, pos, n_tok, dst_offset=pos * kv))
+    torch.cuda.synchronize()
+    _check((qd.cpu().numpy(), q, q_w, kcd.cpu().numpy().view(np.uint16), kc_w,
+            vcd.cpu().numpy().view(np.uint16), vc_w, pos, n_tok))
