@@ -35,7 +35,7 @@ sys.path.insert(0, os.path.join(ROOT, "inference-agent_amd"))
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
 # HBM bytes per C3 decode launch: (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) KiB from rocprofv3, the
 # factors from the copy probe (profiles/attn_decode_C3_traffic.md).
-C3_TRAFFIC_BYTES = int((8463.0 * 2.0 + 456.75) * 1024)
+C3_TRAFFIC_BYTES = int((8465.0 * 2.0 + 456.75) * 1024)
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 MFMA, 2.5 PFLOP/s
 WARMUP_SECONDS = 0.3
 METRIC = "decode-attn HBM GB/s + prefill-attn TFLOPS, Llama-3.2-3B GQA, 1 MI355X"
