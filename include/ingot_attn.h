@@ -43,7 +43,8 @@ extern "C" {
 
 #define INGOT_ATTN_OK 0
 #define INGOT_ATTN_EINVAL (-1)      /* null pointer, zero size, pos/n out of range */
-#define INGOT_ATTN_EUNSUPPORTED (-2) /* head_dim != 128, group size outside 1..4, n_head > 256 */
+#define INGOT_ATTN_EUNSUPPORTED (-2) /* head_dim != 128, group size outside 1..4, n_head > 256;
+                                       linear: weight type or n_in the kernels do not cover */
 #define INGOT_ATTN_EWORKSPACE (-3)  /* workspace smaller than *_workspace_size() */
 #define INGOT_ATTN_EHIP (-4)        /* a HIP runtime call or launch failed */
 

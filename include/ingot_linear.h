@@ -1,0 +1,60 @@
+/*
+ * ingot_linear.h — C ABI of the MI355X (gfx950) linear layer over GGUF weight layouts.
+ *
+ * Replaces `encode_linear` of the Metal backend (src/metal_backend.mm:282-310), used by the
+ * attention output projection with its residual accumulate (`encode_linear(enc, *L.wo, in, x_,
+ * 0, true, n)`, src/metal_backend.mm:446-447) and every other projection of the forward pass;
+ * the CPU path is `ops::matvec` + `x += tmp` (src/ops.cpp:218-225, src/cpu_backend.cpp:71-72).
+ *
+ * Same conventions as ingot_attn.h (device pointers owned by the caller, stream-ordered,
+ * 0 or a negative INGOT_ATTN_E* code). The library is the same libingot_attn.so.
+ *
+ * W keeps the GGUF on-disk layout: ne = [n_in, n_out], row r is n_in elements stored as
+ * n_in / block_size blocks of the tensor type (src/gguf.h:30-33, src/ops.cpp:33-87):
+ *   F32 (0), F16 (1), BF16 (30): plain rows;
+ *   Q8_0 (8): 34-byte blocks of 32; Q4_0 (2): 18-byte blocks of 32; Q4_1 (3): 20-byte blocks
+ *   of 32; Q6_K (14): 210-byte blocks of 256.
+ * These are the types the reference's GPU path has kernels for (src/metal_backend.mm:61-83)
+ * plus BF16, which its CPU path also reads (src/ops.cpp:89-99). Others return
+ * INGOT_ATTN_EUNSUPPORTED, as the reference throws "no matvec kernel for type".
+ *
+ * Numerics: n_tok == 1 computes in f32 from the exact dequantized weights (as ops::matvec and
+ * the Metal matvec kernels); n_tok > 1 rounds x and the dequantized weights to f16 and
+ * accumulates in f32 (as the Metal to_half + matmul path, src/metal_backend.mm:385-392).
+ */
+#ifndef INGOT_LINEAR_H
+#define INGOT_LINEAR_H
+
+#include "ingot_attn.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Mirrors MatvecParams / MatmulParams (shaders/kernels.metal:19, 716: n_in, n_out, n_tok,
+ * out_offset, accumulate) plus the weight type (gguf::TensorInfo::type). */
+typedef struct IngotLinearDesc {
+    uint32_t type;        /* GGUF tensor type id */
+    uint32_t n_in;        /* W.ne[0]; a multiple of 32 (of 256 for Q6_K) */
+    uint32_t n_out;       /* W.ne[1] */
+    uint32_t n_tok;       /* rows of x and of out */
+    uint32_t out_offset;  /* elements added to out */
+    uint32_t accumulate;  /* 0: out = W·x; 1: out += W·x (the residual add after wo) */
+} IngotLinearDesc;
+
+/* Bytes of W for this descriptor (n_out rows of the type's row size), 0 if the descriptor is
+ * invalid or the type unsupported. */
+size_t ingot_linear_weight_bytes(const IngotLinearDesc* d);
+
+/* out[out_offset + t*n_out + r] (+)= sum_k W[r][k] * x[t*n_in + k] for t < n_tok, r < n_out.
+ *   w    weight bytes, 16-byte aligned (GGUF data is 32-byte aligned)
+ *   x    [n_tok][n_in] f32, 16-byte aligned
+ *   out  f32, 4-byte aligned, must not overlap x or w
+ * No workspace. */
+int ingot_linear(const void* w, const float* x, float* out, const IngotLinearDesc* d, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INGOT_LINEAR_H */

@@ -9,6 +9,7 @@
 #include <cstdint>
 
 #include "../../include/ingot_attn.h"
+#include "../../include/ingot_linear.h"
 #include "attn_internal.h"
 
 namespace {
@@ -49,9 +50,55 @@ int check_prefill(const IngotAttnPrefillDesc* d) {
     return INGOT_ATTN_OK;
 }
 
+// Elements per block and bytes per block of the GGUF types with a linear kernel
+// (src/gguf.cpp's type traits); 0 for the others.
+void linear_block(uint32_t type, uint32_t& elems, uint32_t& bytes) {
+    switch (type) {
+        case 0:  elems = 1;   bytes = 4;   return;  // F32
+        case 1:  elems = 1;   bytes = 2;   return;  // F16
+        case 30: elems = 1;   bytes = 2;   return;  // BF16
+        case 8:  elems = 32;  bytes = 34;  return;  // Q8_0
+        case 2:  elems = 32;  bytes = 18;  return;  // Q4_0
+        case 3:  elems = 32;  bytes = 20;  return;  // Q4_1
+        case 14: elems = 256; bytes = 210; return;  // Q6_K
+        default: elems = 0;   bytes = 0;   return;
+    }
+}
+
+int check_linear(const IngotLinearDesc* d) {
+    if (!d || d->n_in == 0 || d->n_out == 0 || d->n_tok == 0) return INGOT_ATTN_EINVAL;
+    uint32_t elems, bytes;
+    linear_block(d->type, elems, bytes);
+    if (elems == 0) return INGOT_ATTN_EUNSUPPORTED;
+    if (d->n_in % 32 != 0 || d->n_in % elems != 0) return INGOT_ATTN_EUNSUPPORTED;
+    if (uint64_t(d->n_in) / elems * bytes > 0x7fffffffull) return INGOT_ATTN_EUNSUPPORTED;
+    if (uint64_t(d->out_offset) + uint64_t(d->n_tok) * d->n_out > 0xffffffffffffull) return INGOT_ATTN_EINVAL;
+    return INGOT_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t ingot_linear_weight_bytes(const IngotLinearDesc* d) {
+    if (check_linear(d)) return 0;
+    uint32_t elems, bytes;
+    linear_block(d->type, elems, bytes);
+    return size_t(d->n_out) * (d->n_in / elems) * bytes;
+}
+
+int ingot_linear(const void* w, const float* x, float* out, const IngotLinearDesc* d, void* stream) {
+    const int rc = check_linear(d);
+    if (rc) return rc;
+    if (!w || !x || !out) return INGOT_ATTN_EINVAL;
+    if (!aligned16(w) || !aligned16(x) || (reinterpret_cast<uintptr_t>(out) & 3u) != 0)
+        return INGOT_ATTN_EINVAL;
+    const int lrc = ingot::launch_linear(d->type, w, x, out + d->out_offset, d->n_in, d->n_out,
+                                         d->n_tok, d->accumulate ? 1u : 0u,
+                                         static_cast<hipStream_t>(stream));
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
+         : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
+}
 
 uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
     if (check_decode(d)) return 0;
@@ -144,7 +191,7 @@ const char* ingot_attn_strerror(int code) {
     switch (code) {
         case INGOT_ATTN_OK: return "ok";
         case INGOT_ATTN_EINVAL: return "invalid argument (null/misaligned pointer, zero size or position out of range)";
-        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (head_dim must be 128, n_head/n_head_kv in 1..4, n_head <= 256)";
+        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (attention: head_dim 128, n_head/n_head_kv in 1..4, n_head <= 256; linear: weight type without a kernel or n_in not a multiple of its block)";
         case INGOT_ATTN_EWORKSPACE: return "workspace smaller than the *_workspace_size() figure";
         case INGOT_ATTN_EHIP: return "HIP launch failed";
         default: return "unknown error";

@@ -34,4 +34,9 @@ int launch_rope_kv_store(float* q, const float* k, const float* v, _Float16* k_c
                          uint32_t n_head_kv, uint32_t head_dim, uint32_t pos, uint32_t n_tok,
                          uint32_t q_stride, uint32_t kv_stride, hipStream_t stream);
 
+// out (+)= W·x over a GGUF weight layout (type id as in ggml). Returns 0, -1 (grid too large),
+// -2 (type without a kernel) or -4 (launch failed).
+int launch_linear(uint32_t type, const void* W, const float* x, float* out, uint32_t n_in,
+                  uint32_t n_out, uint32_t n_tok, uint32_t accumulate, hipStream_t stream);
+
 }  // namespace ingot

@@ -1,4 +1,5 @@
-"""ctypes binding of libingot_attn.so, the C ABI declared in include/ingot_attn.h.
+"""ctypes binding of libingot_attn.so, the C ABI declared in include/ingot_attn.h and
+include/ingot_linear.h.
 
 This is the host-side mirror of the attention step of Ingot's `Backend` (src/backend.h:9-23;
 the Metal dispatcher is `encode_attention`, src/metal_backend.mm:336-383). Device memory and
@@ -16,7 +17,7 @@ from ctypes import c_float, c_int, c_size_t, c_uint32, c_uint64, c_void_p
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libingot_attn.so")
 
-# Exported symbols, as declared in include/ingot_attn.h.
+# Exported symbols, as declared in include/ingot_attn.h and include/ingot_linear.h.
 EXPORTS = (
     "ingot_attn_decode_workspace_size",
     "ingot_attn_prefill_workspace_size",
@@ -27,7 +28,14 @@ EXPORTS = (
     "ingot_rope_kv_store",
     "ingot_attn_strerror",
     "ingot_attn_version",
+    "ingot_linear_weight_bytes",
+    "ingot_linear",
 )
+
+# GGUF tensor type ids (ggml's enum, src/gguf.h:30-33) with a linear kernel, and their
+# (elements, bytes) per block (src/ops.cpp:33-87).
+GGUF_TYPES = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q8_0": 8, "Q6_K": 14, "BF16": 30}
+BLOCK = {0: (1, 4), 1: (1, 2), 30: (1, 2), 8: (32, 34), 2: (32, 18), 3: (32, 20), 14: (256, 210)}
 
 
 class DecodeDesc(ctypes.Structure):
@@ -75,6 +83,19 @@ class RopeKvDesc(ctypes.Structure):
     ]
 
 
+class LinearDesc(ctypes.Structure):
+    """IngotLinearDesc; mirrors MatvecParams / MatmulParams (shaders/kernels.metal:19, 716)."""
+
+    _fields_ = [
+        ("type", c_uint32),
+        ("n_in", c_uint32),
+        ("n_out", c_uint32),
+        ("n_tok", c_uint32),
+        ("out_offset", c_uint32),
+        ("accumulate", c_uint32),
+    ]
+
+
 _lib = None
 
 
@@ -104,6 +125,10 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ingot_attn_prefill.restype = c_int
     lib.ingot_rope_kv_store.argtypes = [c_void_p] * 6 + [ctypes.POINTER(RopeKvDesc), c_void_p]
     lib.ingot_rope_kv_store.restype = c_int
+    lib.ingot_linear_weight_bytes.argtypes = [ctypes.POINTER(LinearDesc)]
+    lib.ingot_linear_weight_bytes.restype = c_size_t
+    lib.ingot_linear.argtypes = [c_void_p] * 3 + [ctypes.POINTER(LinearDesc), c_void_p]
+    lib.ingot_linear.restype = c_int
     lib.ingot_attn_strerror.argtypes = [c_int]
     lib.ingot_attn_strerror.restype = ctypes.c_char_p
     lib.ingot_attn_version.argtypes = []
@@ -228,3 +253,26 @@ def rope_kv_store(q, k, v, k_cache, v_cache, inv_freq, desc: RopeKvDesc, stream=
         c_void_p(v.data_ptr()), c_void_p(k_cache.data_ptr()), c_void_p(v_cache.data_ptr()),
         c_void_p(inv_freq.data_ptr()), ctypes.byref(desc), _stream_ptr(stream))
     _check(rc, "ingot_rope_kv_store")
+
+
+def linear_desc(type_, n_in, n_out, n_tok=1, out_offset=0, accumulate=False):
+    t = GGUF_TYPES[type_] if isinstance(type_, str) else int(type_)
+    return LinearDesc(t, n_in, n_out, n_tok, out_offset, 1 if accumulate else 0)
+
+
+def linear_weight_bytes(desc: LinearDesc) -> int:
+    return int(load_library().ingot_linear_weight_bytes(ctypes.byref(desc)))
+
+
+def linear(w, x, out, desc: LinearDesc, stream=None):
+    """out[out_offset + t*n_out + r] (+)= W[r]·x[t] over the GGUF weight bytes `w`.
+
+    w: uint8 CUDA tensor of the raw weight bytes (ingot_linear_weight_bytes long); x, out: f32
+    CUDA tensors. Replaces encode_linear (src/metal_backend.mm:282-310); with accumulate it is
+    the wo projection plus residual add (src/metal_backend.mm:446-447).
+    """
+    lib = load_library()
+    rc = lib.ingot_linear(c_void_p(w.data_ptr()), c_void_p(x.data_ptr()), c_void_p(out.data_ptr()),
+                          ctypes.byref(desc), _stream_ptr(stream))
+    _check(rc, "ingot_linear")
+    return out

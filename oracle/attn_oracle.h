@@ -37,6 +37,16 @@ int oracle_rope_kv_store(float* q, int q_stride, int n_head, const float* k, con
                          int kv_stride, uint16_t* k_cache, uint16_t* v_cache, size_t dst_offset,
                          int n_head_kv, int head_dim, int pos, int n_tok, const float* inv_freq);
 
+// Linear layer over a GGUF weight layout (linear_oracle.cpp). type = GGUF type id (F32 0,
+// F16 1, Q4_0 2, Q4_1 3, Q8_0 8, Q6_K 14, BF16 30). out[t*n_out + r] (+)= W[r]·x[t].
+// oracle_linear follows ops::matvec (f32); oracle_linear_f16 the Metal batched path (x and
+// weights rounded to f16). Return 0 or -1.
+int oracle_dequant_row(int type, const uint8_t* row, float* out, int n);
+int oracle_linear(int type, const uint8_t* w, const float* x, float* out, int n_in, int n_out,
+                  int n_tok, int accumulate, int n_threads);
+int oracle_linear_f16(int type, const uint8_t* w, const float* x, float* out, int n_in, int n_out,
+                      int n_tok, int accumulate, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,11 @@ def lib() -> ctypes.CDLL:
         L.oracle_rope_kv_store.argtypes = ([c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p,
                                             c_void_p, c_size_t] + [c_int] * 4 + [c_void_p])
         L.oracle_rope_kv_store.restype = c_int
+        L.oracle_dequant_row.argtypes = [c_int, c_void_p, c_void_p, c_int]
+        L.oracle_dequant_row.restype = c_int
+        for f in (L.oracle_linear, L.oracle_linear_f16):
+            f.argtypes = [c_int, c_void_p, c_void_p, c_void_p] + [c_int] * 5
+            f.restype = c_int
         _lib = L
     return _lib
 
@@ -127,3 +132,49 @@ def rope_kv_store(q, k, v, k_cache, v_cache, dst_offset, n_head, n_head_kv, head
     if rc != 0:
         raise ValueError("oracle_rope_kv_store: bad arguments")
     return qq, kc, vc
+
+
+# GGUF type ids and (elements, bytes) per block, as in the library (src/gguf.h:30-33).
+GGUF_TYPES = {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q8_0": 8, "Q6_K": 14, "BF16": 30}
+BLOCK = {0: (1, 4), 1: (1, 2), 30: (1, 2), 8: (32, 34), 2: (32, 18), 3: (32, 20), 14: (256, 210)}
+
+
+def _type_id(t):
+    return GGUF_TYPES[t] if isinstance(t, str) else int(t)
+
+
+def dequant_rows(type_, w: np.ndarray, n_in: int) -> np.ndarray:
+    """Dequantizes every row of the weight bytes w ([n_out][row_bytes] uint8) to f32."""
+    t = _type_id(type_)
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1)
+    be, bb = BLOCK[t]
+    if n_in <= 0 or n_in % be:
+        raise ValueError(f"n_in={n_in} is not a multiple of the block size {be}")
+    row_bytes = n_in // be * bb
+    n_out = w.size // row_bytes
+    out = np.empty((n_out, n_in), dtype=np.float32)
+    for r in range(n_out):
+        rc = lib().oracle_dequant_row(t, c_void_p(w.ctypes.data + r * row_bytes),
+                                      c_void_p(out[r].ctypes.data), n_in)
+        if rc != 0:
+            raise ValueError("oracle_dequant_row: bad argument")
+    return out
+
+
+def linear(type_, w: np.ndarray, x: np.ndarray, n_in: int, n_out: int, out=None, accumulate=False,
+           f16_path=False, n_threads=None) -> np.ndarray:
+    """out[t][r] (+)= W[r]·x[t] (ops::matvec; f16_path: the Metal batched numerics)."""
+    t = _type_id(type_)
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, n_in)
+    n_tok = x.shape[0]
+    if out is None:
+        out = np.zeros((n_tok, n_out), dtype=np.float32)
+    else:
+        out = np.ascontiguousarray(out, dtype=np.float32).reshape(n_tok, n_out).copy()
+    f = lib().oracle_linear_f16 if f16_path else lib().oracle_linear
+    rc = f(t, _ptr(w), _ptr(x), _ptr(out), n_in, n_out, n_tok, 1 if accumulate else 0,
+           n_threads or min(8, os.cpu_count() or 1))
+    if rc != 0:
+        raise ValueError("oracle_linear: bad argument")
+    return out

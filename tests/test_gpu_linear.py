@@ -1,0 +1,144 @@
+"""GPU parity of the linear layer (ingot_linear) against the CPU oracle, every weight type.
+
+Tolerances, stated per path:
+  - one token (matvec, f32 arithmetic on exactly dequantized weights): against oracle_linear
+    (ops::matvec), rel-L2 <= 1e-5 and max|d| <= 1e-5 * max|ref| + 1e-6 — only the order of the
+    f32 sums differs;
+  - several tokens (MFMA matmul, x and weights rounded to f16 as the reference's Metal batched
+    path does): against oracle_linear_f16 (the same two roundings on the CPU), rel-L2 <= 1e-5 and
+    max|d| <= 1e-5 * max|ref| + 1e-6; against the f32 CPU path
+    max|d| <= 2e-3 and rel-L2 <= 1e-3 (outputs are O(1): x ~ N(0,1), W rows of norm ~1);
+  - out_offset and accumulate: out = base + W·x in the addressed range, every element outside
+    it keeps its NaN canary bits.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import assert_parity, ensure_built
+
+import gguf_blocks as gb
+
+pytestmark = pytest.mark.gpu
+
+TYPES = ["F32", "F16", "BF16", "Q8_0", "Q4_0", "Q4_1", "Q6_K"]
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a GPU")
+    ensure_built("lib")
+    import ingot_attn
+
+    ingot_attn.load_library()
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _run(dev, t, raw, x, n_in, n_out, base=None, out_offset=0, pad=37):
+    """Runs ingot_linear; returns (result [n_tok][n_out], the whole out buffer)."""
+    import torch
+    import ingot_attn as ia
+
+    n_tok = x.shape[0]
+    total = out_offset + n_tok * n_out + pad
+    buf = np.full(total, np.nan, dtype=np.float32)
+    if base is not None:
+        buf[out_offset:out_offset + n_tok * n_out] = base.ravel()
+    out = _t(buf, dev)
+    d = ia.linear_desc(t, n_in, n_out, n_tok, out_offset=out_offset, accumulate=base is not None)
+    assert ia.linear_weight_bytes(d) == raw.size
+    ia.linear(_t(raw.reshape(-1), dev), _t(x, dev), out, d)
+    torch.cuda.synchronize()
+    full = out.cpu().numpy()
+    return full[out_offset:out_offset + n_tok * n_out].reshape(n_tok, n_out), full
+
+
+def _close(got, want, what):
+    d = np.abs(got.astype(np.float64) - want)
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    tol = 1e-5 * np.abs(want).max() + 1e-6
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert d.max() <= tol and rel <= 1e-5, f"{what}: max|d|={d.max():.3e} (tol {tol:.1e}), rel-L2={rel:.3e}"
+
+
+def _x(n_tok, n_in, seed):
+    return np.random.default_rng(seed).standard_normal((n_tok, n_in)).astype(np.float32)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in,n_out", [(3072, 3072), (256, 200), (8192, 96), (512, 1001)])
+def test_matvec(dev, oracle_mod, t, n_in, n_out):
+    raw = gb.random_weights(t, n_out, n_in, seed=n_in + n_out)
+    x = _x(1, n_in, seed=1)
+    got, _ = _run(dev, t, raw, x, n_in, n_out)
+    _close(got, oracle_mod.linear(t, raw, x, n_in, n_out), f"{t} matvec {n_in}x{n_out}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_tok,n_in,n_out", [(2, 256, 256), (37, 512, 300), (64, 1024, 512),
+                                              (130, 768, 257)])
+def test_matmul(dev, oracle_mod, t, n_tok, n_in, n_out):
+    raw = gb.random_weights(t, n_out, n_in, seed=n_tok + n_in)
+    x = _x(n_tok, n_in, seed=2)
+    got, _ = _run(dev, t, raw, x, n_in, n_out)
+    _close(got, oracle_mod.linear(t, raw, x, n_in, n_out, f16_path=True),
+           f"{t} matmul {n_tok}x{n_in}x{n_out}")
+    assert_parity(got, oracle_mod.linear(t, raw, x, n_in, n_out), f"{t} matmul vs f32 path")
+
+
+@pytest.mark.parametrize("t", ["F16", "Q4_0", "Q8_0", "Q6_K"])
+def test_wo_prefill_shape(dev, oracle_mod, t):
+    """The attention output projection at the 512-token prefill chunk, with the residual add."""
+    n_tok, n = 512, 3072
+    raw = gb.random_weights(t, n, n, seed=11)
+    x = _x(n_tok, n, seed=12)
+    base = _x(n_tok, n, seed=13)
+    got, _ = _run(dev, t, raw, x, n, n, base=base)
+    want = oracle_mod.linear(t, raw, x, n, n, out=base, accumulate=True, f16_path=True)
+    _close(got, want, f"{t} wo 512x3072x3072")
+
+
+@pytest.mark.parametrize("n_tok", [1, 5])
+def test_offset_and_accumulate(dev, oracle_mod, n_tok):
+    t, n_in, n_out, off = "Q4_0", 512, 96, 1234
+    raw = gb.random_weights(t, n_out, n_in, seed=21)
+    x = _x(n_tok, n_in, seed=22)
+    base = _x(n_tok, n_out, seed=23)
+    got, full = _run(dev, t, raw, x, n_in, n_out, base=base, out_offset=off)
+    want = oracle_mod.linear(t, raw, x, n_in, n_out, out=base, accumulate=True, f16_path=n_tok > 1)
+    _close(got, want, f"accumulate n_tok={n_tok}")
+    assert np.all(np.isnan(full[:off])) and np.all(np.isnan(full[off + n_tok * n_out:]))
+    # without accumulate the previous contents are ignored
+    got2, _ = _run(dev, t, raw, x, n_in, n_out, out_offset=off)
+    _close(got2, oracle_mod.linear(t, raw, x, n_in, n_out, f16_path=n_tok > 1), "overwrite")
+
+
+def test_errors(dev):
+    import torch
+    import ingot_attn as ia
+
+    lib = ia.load_library()
+    w = torch.zeros(4096, dtype=torch.uint8, device=dev)
+    x = torch.zeros(256, dtype=torch.float32, device=dev)
+    o = torch.zeros(256, dtype=torch.float32, device=dev)
+    import ctypes
+
+    def call(d):
+        return lib.ingot_linear(ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(x.data_ptr()),
+                                ctypes.c_void_p(o.data_ptr()), ctypes.byref(d), None)
+
+    assert call(ia.linear_desc(6, 256, 4)) == -2          # Q5_0: no kernel
+    assert call(ia.linear_desc("Q6_K", 128, 4)) == -2     # n_in not a multiple of 256
+    assert call(ia.linear_desc("F16", 0, 4)) == -1
+    assert call(ia.linear_desc("F16", 256, 4)) == 0
+    torch.cuda.synchronize()
