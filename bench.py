@@ -18,7 +18,9 @@ rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy kernel of known size
 
 The same line carries the prefill figures (C4, C5-prefill, C2: TFLOPS and fractions of the
 f16-MFMA and HBM peaks), the decode sweep (C1, C5 lengths), the fused RoPE + KV-cache store
-that precedes attention (GB/s for a 512-token chunk and one decode token) and the CPU baseline
+that precedes attention (GB/s for a 512-token chunk and one decode token), the attention output
+projection wo with its residual add (GB/s for one token, TFLOPS for a 512-token chunk, four
+GGUF weight types) and the CPU baseline
 (the oracle, a C++ restatement of Ingot's CPU attention, on the host cores).
 """
 from __future__ import annotations
@@ -45,6 +47,11 @@ DECODE = {"c3": ("C3-decode-4096", 4096, 0.5, 3), "c1": ("C1-decode-512", 512, 1
           "c5d1k": ("C5-decode-1024", 1024, 1.0, 50), "c5d2k": ("C5-decode-2048", 2048, 1.0, 51),
           "c5d8k": ("C5-decode-8192", 8192, 1.0, 53)}
 PREFILL = {"c4": "C4-prefill-512@3584", "c5p": "C5-prefill-2048@6144", "c2": "C2-prefill-512@0"}
+# name -> (weight type, n_tok): the attention output projection wo (3072 x 3072) with the residual
+# add, for one decode token and a 512-token prefill chunk
+LINEAR = {"wo1-f16": ("F16", 1), "wo1-q8": ("Q8_0", 1), "wo1-q4": ("Q4_0", 1), "wo1-q6k": ("Q6_K", 1),
+          "wo512-f16": ("F16", 512), "wo512-q8": ("Q8_0", 512), "wo512-q4": ("Q4_0", 512),
+          "wo512-q6k": ("Q6_K", 512)}
 # name -> (pos, n_tok): the KV-store step before attention, for a prefill chunk and a decode token
 KVSTORE = {"kv512": ("kv-store-512@3584", 3584, 512), "kv1": ("kv-store-1@4095", 4095, 1)}
 
@@ -55,7 +62,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    help="all | decode | prefill | kvstore | one of " + ", ".join(list(DECODE) + list(PREFILL) + list(KVSTORE)))
+                    help="all | decode | prefill | kvstore | linear | one of "
+                    + ", ".join(list(DECODE) + list(PREFILL) + list(KVSTORE) + list(LINEAR)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -145,6 +153,35 @@ class KvStoreBench:
             self.ia.rope_kv_store(self.q, self.k, self.v, self.kc, self.vc, self.inv, d)
 
 
+class LinearBench:
+    """ingot_linear for wo (n_in = n_out = 3072) with accumulate, one call per weight copy per
+    step. The weight bytes are replicated into enough copies (>= 28, >= 1 GiB together) that
+    the reads come from HBM rather than the 256 MB last-level cache. Algorithmic bytes per call:
+    the weights, x (f32) and out read and written (f32); flops: 2 * n_tok * n_in * n_out."""
+
+    def __init__(self, torch, ia, gb, t, n_tok, seed, n_in=3072, n_out=3072):
+        dev = torch.device("cuda:0")
+        raw = gb.random_weights(t, n_out, n_in, seed=seed).reshape(-1)
+        wb = raw.size
+        pitch = (wb + 255) // 256 * 256
+        self.n_copies = max(28, -(-(1 << 30) // pitch))
+        one = torch.from_numpy(raw).to(dev)
+        self.w = torch.empty(self.n_copies, pitch, dtype=torch.uint8, device=dev)
+        self.w[:, :wb] = one
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        self.x = torch.randn(n_tok, n_in, generator=g, device=dev)
+        self.out = torch.randn(n_tok, n_out, generator=g, device=dev)
+        self.desc = ia.linear_desc(t, n_in, n_out, n_tok, accumulate=True)
+        self.ia = ia
+        self.nbytes = wb + 4 * n_tok * (n_in + 2 * n_out)
+        self.flops = 2 * n_tok * n_in * n_out
+
+    def step(self):
+        for i in range(self.n_copies):
+            self.ia.linear(self.w[i], self.x, self.out, self.desc)
+
+
 def time_steps(torch, fn, steps, warmup, use_graph):
     """Seconds per step over `steps` timed steps (after `warmup`), graph-replayed by default."""
     stream = torch.cuda.current_stream()
@@ -215,7 +252,7 @@ def main():
     use_graph = not args.no_graph
     sel = args.only
     want = lambda key, group: sel in ("all", group, key)
-    res = {"decode": {}, "prefill": {}, "kv_store": {}}
+    res = {"decode": {}, "prefill": {}, "kv_store": {}, "linear": {}}
 
     head = None
     for key, (name, n_keys, kv_scale, seed) in DECODE.items():
@@ -262,6 +299,24 @@ def main():
         gbs = b.nbytes / sps / 1e9
         res["kv_store"][name] = {"us_per_call": round(sps * 1e6, 3), "GB/s": round(gbs, 1),
                                  "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "bytes_per_call": b.nbytes}
+        del b
+        torch.cuda.empty_cache()
+
+    import gguf_blocks as gb
+
+    for key, (t, n_tok) in LINEAR.items():
+        if not want(key, "linear"):
+            continue
+        b = LinearBench(torch, ia, gb, t, n_tok, 31)
+        steps = max(5, args.steps // 5)
+        sps = time_steps(torch, b.step, steps, args.warmup, use_graph) / b.n_copies
+        gbs = b.nbytes / sps / 1e9
+        tfs = b.flops / sps / 1e12
+        res["linear"][f"wo-{t}-{n_tok}tok"] = {
+            "us_per_call": round(sps * 1e6, 3), "GB/s": round(gbs, 1),
+            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4), "TFLOPS": round(tfs, 2),
+            "mfma_frac": round(tfs / MFMA_F16_PEAK_TFS, 4), "bytes_per_call": b.nbytes,
+            "flops_per_call": b.flops}
         del b
         torch.cuda.empty_cache()
 

@@ -32,7 +32,8 @@ extern "C" {
 #endif
 
 /* Mirrors MatvecParams / MatmulParams (shaders/kernels.metal:19, 716: n_in, n_out, n_tok,
- * out_offset, accumulate) plus the weight type (gguf::TensorInfo::type). */
+ * out_offset, accumulate) plus the weight type (gguf::TensorInfo::type) and, as in the
+ * attention descriptors, a requested split count for the batched path. */
 typedef struct IngotLinearDesc {
     uint32_t type;        /* GGUF tensor type id */
     uint32_t n_in;        /* W.ne[0]; a multiple of 32 (of 256 for Q6_K) */
@@ -40,18 +41,38 @@ typedef struct IngotLinearDesc {
     uint32_t n_tok;       /* rows of x and of out */
     uint32_t out_offset;  /* elements added to out */
     uint32_t accumulate;  /* 0: out = W·x; 1: out += W·x (the residual add after wo) */
+    uint32_t n_splits;    /* n_tok > 1: ways to split n_in across workgroups; 0 = library's
+                             choice, 1 = never; at most 8 */
 } IngotLinearDesc;
 
 /* Bytes of W for this descriptor (n_out rows of the type's row size), 0 if the descriptor is
  * invalid or the type unsupported. */
 size_t ingot_linear_weight_bytes(const IngotLinearDesc* d);
 
+/* Split count the call with this descriptor and a large enough workspace would use (1 for
+ * n_tok == 1 or no split), 0 for an invalid descriptor. */
+uint32_t ingot_linear_splits(const IngotLinearDesc* d);
+
+/* Bytes of device workspace that lets the batched path (n_tok > 1) split the reduction over
+ * n_in across workgroups when the output alone has too few tiles to fill the GPU. The
+ * workspace must be zero-filled once when it is allocated (it holds completion counters that
+ * every call leaves at zero again); one workspace of the largest size serves every smaller
+ * call. Returns 0 for an invalid descriptor. */
+size_t ingot_linear_workspace_size(const IngotLinearDesc* d);
+
 /* out[out_offset + t*n_out + r] (+)= sum_k W[r][k] * x[t*n_in + k] for t < n_tok, r < n_out.
- *   w    weight bytes, 16-byte aligned (GGUF data is 32-byte aligned)
- *   x    [n_tok][n_in] f32, 16-byte aligned
- *   out  f32, 4-byte aligned, must not overlap x or w
- * No workspace. */
-int ingot_linear(const void* w, const float* x, float* out, const IngotLinearDesc* d, void* stream);
+ *   w          weight bytes, 16-byte aligned (GGUF data is 32-byte aligned)
+ *   x          [n_tok][n_in] f32, 16-byte aligned
+ *   out        f32, 4-byte aligned, must not overlap x or w
+ *   workspace  NULL (n_in is never split) or 16-byte aligned device memory of workspace_bytes;
+ *              with less than ingot_linear_workspace_size() bytes the call splits less or not
+ *              at all.
+ * Deterministic: the split partials are summed in a fixed order, so equal inputs and equal
+ * workspace sizes give bit-identical results; calls with and without a split differ by f32
+ * rounding only. Not thread-safe per workspace (calls sharing one must be ordered on a
+ * stream). */
+int ingot_linear(const void* w, const float* x, float* out, void* workspace, size_t workspace_bytes,
+                 const IngotLinearDesc* d, void* stream);
 
 #ifdef __cplusplus
 }

@@ -73,6 +73,7 @@ int check_linear(const IngotLinearDesc* d) {
     if (d->n_in % 32 != 0 || d->n_in % elems != 0) return INGOT_ATTN_EUNSUPPORTED;
     if (uint64_t(d->n_in) / elems * bytes > 0x7fffffffull) return INGOT_ATTN_EUNSUPPORTED;
     if (uint64_t(d->out_offset) + uint64_t(d->n_tok) * d->n_out > 0xffffffffffffull) return INGOT_ATTN_EINVAL;
+    if (d->n_splits > 8) return INGOT_ATTN_EINVAL;
     return INGOT_ATTN_OK;
 }
 
@@ -87,14 +88,27 @@ size_t ingot_linear_weight_bytes(const IngotLinearDesc* d) {
     return size_t(d->n_out) * (d->n_in / elems) * bytes;
 }
 
-int ingot_linear(const void* w, const float* x, float* out, const IngotLinearDesc* d, void* stream) {
+uint32_t ingot_linear_splits(const IngotLinearDesc* d) {
+    if (check_linear(d)) return 0;
+    return ingot::linear_splits(d->n_in, d->n_out, d->n_tok, d->n_splits, ~size_t(0));
+}
+
+size_t ingot_linear_workspace_size(const IngotLinearDesc* d) {
+    if (check_linear(d)) return 0;
+    return ingot::linear_workspace_size(d->n_in, d->n_out, d->n_tok, d->n_splits);
+}
+
+int ingot_linear(const void* w, const float* x, float* out, void* workspace, size_t workspace_bytes,
+                 const IngotLinearDesc* d, void* stream) {
     const int rc = check_linear(d);
     if (rc) return rc;
     if (!w || !x || !out) return INGOT_ATTN_EINVAL;
     if (!aligned16(w) || !aligned16(x) || (reinterpret_cast<uintptr_t>(out) & 3u) != 0)
         return INGOT_ATTN_EINVAL;
+    if (workspace && !aligned16(workspace)) return INGOT_ATTN_EINVAL;
     const int lrc = ingot::launch_linear(d->type, w, x, out + d->out_offset, d->n_in, d->n_out,
-                                         d->n_tok, d->accumulate ? 1u : 0u,
+                                         d->n_tok, d->accumulate ? 1u : 0u, d->n_splits, workspace,
+                                         workspace ? workspace_bytes : 0,
                                          static_cast<hipStream_t>(stream));
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
          : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;

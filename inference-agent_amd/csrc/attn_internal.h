@@ -34,9 +34,20 @@ int launch_rope_kv_store(float* q, const float* k, const float* v, _Float16* k_c
                          uint32_t n_head_kv, uint32_t head_dim, uint32_t pos, uint32_t n_tok,
                          uint32_t q_stride, uint32_t kv_stride, hipStream_t stream);
 
-// out (+)= W·x over a GGUF weight layout (type id as in ggml). Returns 0, -1 (grid too large),
-// -2 (type without a kernel) or -4 (launch failed).
+// Linear layer workspace: split-K completion counters (one 64-byte line per output tile, for up
+// to kLinearMaxTiles tiles), then the partial tiles.
+constexpr size_t kLinearCounterBytes = 16384;
+constexpr uint32_t kLinearMaxTiles = 256;
+
+// out (+)= W·x over a GGUF weight layout (type id as in ggml). With a workspace (zero-filled
+// once) the batched path may split K across workgroups; without one it never does.
+// Returns 0, -1 (grid too large), -2 (type without a kernel) or -4 (launch failed).
 int launch_linear(uint32_t type, const void* W, const float* x, float* out, uint32_t n_in,
-                  uint32_t n_out, uint32_t n_tok, uint32_t accumulate, hipStream_t stream);
+                  uint32_t n_out, uint32_t n_tok, uint32_t accumulate, uint32_t n_splits,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream);
+// Split count for the batched path (requested: 0 = choose); `workspace_bytes` bounds it.
+uint32_t linear_splits(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested,
+                       size_t workspace_bytes);
+size_t linear_workspace_size(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested);
 
 }  // namespace ingot

@@ -193,188 +193,268 @@ __global__ __launch_bounds__(256) void linear_matvec_kernel(
 
 // ---------------------------------------------------------------- several tokens
 
+constexpr int kMmWaves = 8;
 constexpr int kMmToks = 64;        // tokens per workgroup
-constexpr int kMmRowsWave = 64;    // weight rows per wave
-constexpr int kMmRows = 4 * kMmRowsWave;
+constexpr int kMmRowsWave = 32;    // weight rows per wave (one 32-wide MFMA column block)
+constexpr int kMmRows = kMmWaves * kMmRowsWave;
 constexpr int kMmK = 32;           // k per step
 constexpr int kXPitch = kMmK + 8;  // f16 elements per staged token row (80 B: conflict-free b128 reads)
 
-// Raw weight bytes of one lane for one k step: row-block j (rows 32j + lane%32 of the wave),
-// elements k0 + 16s + 8h + i (h = lane/32, s = 0, 1; i = 0..7).
+// Raw weight bytes of one lane for one k step: row rowbase + lane%32 of the wave, elements
+// k0 + 16s + 8h + i (h = lane/32, s = 0, 1; i = 0..7) — the B operands of the step's two
+// 32x32x16 MFMAs.
 template <int T> struct Raw;
-template <> struct Raw<kF32>  { float4v v[2][2][2]; };
-template <> struct Raw<kF16>  { half8 v[2][2]; };
-template <> struct Raw<kBF16> { u32x4 v[2][2]; };
-template <> struct Raw<kQ8_0> { uint32_t d[2]; uint32_t q[2][2][2]; };
-template <> struct Raw<kQ4_0> { uint32_t d[2]; uint32_t q[2][2]; };
-template <> struct Raw<kQ4_1> { uint32_t d[2]; uint32_t m[2]; uint32_t q[2][2]; };
-template <> struct Raw<kQ6_K> { uint32_t d[2]; uint32_t sc[2]; uint32_t ql[2][2][2]; uint32_t qh[2][2][2]; };
+template <> struct Raw<kF32>  { float4v v[2][2]; };
+template <> struct Raw<kF16>  { half8 v[2]; };
+template <> struct Raw<kBF16> { u32x4 v[2]; };
+template <> struct Raw<kQ8_0> { uint32_t d; uint32_t q[2][2]; };
+template <> struct Raw<kQ4_0> { uint32_t d; uint32_t q[2]; };
+template <> struct Raw<kQ4_1> { uint32_t d; uint32_t m; uint32_t q[2]; };
+template <> struct Raw<kQ6_K> { uint32_t d; uint32_t sc; uint32_t ql[2][2]; uint32_t qh[2][2]; };
 
 template <int T>
-__device__ __forceinline__ void load_raw(Raw<T>& r, const uint8_t* const rows[2], uint32_t k0, uint32_t h) {
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const uint8_t* row = rows[j];
-        if constexpr (T == kF32) {
-            for (int s = 0; s < 2; s++) {
-                const float4v* p = reinterpret_cast<const float4v*>(row + 4 * (k0 + 16 * s + 8 * h));
-                r.v[j][s][0] = p[0];
-                r.v[j][s][1] = p[1];
-            }
-        } else if constexpr (T == kF16 || T == kBF16) {
-            for (int s = 0; s < 2; s++) {
-                const uint8_t* p = row + 2 * (k0 + 16 * s + 8 * h);
-                if constexpr (T == kF16) r.v[j][s] = *reinterpret_cast<const half8*>(p);
-                else r.v[j][s] = *reinterpret_cast<const u32x4*>(p);
-            }
-        } else if constexpr (T == kQ8_0) {
-            const uint8_t* b = row + 34 * (k0 / 32);
-            r.d[j] = ld_u16(b);
-            for (int s = 0; s < 2; s++) ld_8bytes(b + 2 + 16 * s + 8 * h, r.q[j][s][0], r.q[j][s][1]);
-        } else if constexpr (T == kQ4_0 || T == kQ4_1) {
-            constexpr int kBytes = T == kQ4_0 ? 18 : 20, kQs = T == kQ4_0 ? 2 : 4;
-            const uint8_t* b = row + kBytes * (k0 / 32);
-            r.d[j] = ld_u16(b);
-            if constexpr (T == kQ4_1) r.m[j] = ld_u16(b + 2);
-            ld_8bytes(b + kQs + 8 * h, r.q[j][0], r.q[j][1]);
-        } else if constexpr (T == kQ6_K) {
-            const uint8_t* b = row + 210 * (k0 / 256);
-            const uint32_t e = k0 % 256, hh = e / 128, g = (e % 128) / 32;
-            r.d[j] = ld_u16(b + 208);
-            r.sc[j] = ld_u16(b + 192 + hh * 8 + 2 * g);  // scales for s = 0 (low byte) and 1
-            for (int s = 0; s < 2; s++) {
-                const uint32_t l = 16 * s + 8 * h;
-                ld_8bytes(b + hh * 64 + 32 * (g & 1) + l, r.ql[j][s][0], r.ql[j][s][1]);
-                ld_8bytes(b + 128 + hh * 32 + l, r.qh[j][s][0], r.qh[j][s][1]);
-            }
+__device__ __forceinline__ void load_raw(Raw<T>& r, const uint8_t* row, uint32_t k0, uint32_t h) {
+    if constexpr (T == kF32) {
+        for (int s = 0; s < 2; s++) {
+            const float4v* p = reinterpret_cast<const float4v*>(row + 4 * (k0 + 16 * s + 8 * h));
+            r.v[s][0] = p[0];
+            r.v[s][1] = p[1];
+        }
+    } else if constexpr (T == kF16 || T == kBF16) {
+        for (int s = 0; s < 2; s++) {
+            const uint8_t* p = row + 2 * (k0 + 16 * s + 8 * h);
+            if constexpr (T == kF16) r.v[s] = *reinterpret_cast<const half8*>(p);
+            else r.v[s] = *reinterpret_cast<const u32x4*>(p);
+        }
+    } else if constexpr (T == kQ8_0) {
+        const uint8_t* b = row + 34 * (k0 / 32);
+        r.d = ld_u16(b);
+        for (int s = 0; s < 2; s++) ld_8bytes(b + 2 + 16 * s + 8 * h, r.q[s][0], r.q[s][1]);
+    } else if constexpr (T == kQ4_0 || T == kQ4_1) {
+        constexpr int kBytes = T == kQ4_0 ? 18 : 20, kQs = T == kQ4_0 ? 2 : 4;
+        const uint8_t* b = row + kBytes * (k0 / 32);
+        r.d = ld_u16(b);
+        if constexpr (T == kQ4_1) r.m = ld_u16(b + 2);
+        ld_8bytes(b + kQs + 8 * h, r.q[0], r.q[1]);
+    } else if constexpr (T == kQ6_K) {
+        const uint8_t* b = row + 210 * (k0 / 256);
+        const uint32_t e = k0 % 256, hh = e / 128, g = (e % 128) / 32;
+        r.d = ld_u16(b + 208);
+        r.sc = ld_u16(b + 192 + hh * 8 + 2 * g);  // scales for s = 0 (low byte) and 1
+        for (int s = 0; s < 2; s++) {
+            const uint32_t l = 16 * s + 8 * h;
+            ld_8bytes(b + hh * 64 + 32 * (g & 1) + l, r.ql[s][0], r.ql[s][1]);
+            ld_8bytes(b + 128 + hh * 32 + l, r.qh[s][0], r.qh[s][1]);
         }
     }
 }
 
-// The f16 B fragment of row-block j, step s.
+// The f16 B fragment of step half s.
 template <int T>
-__device__ __forceinline__ half8 frag(const Raw<T>& r, int j, int s, uint32_t k0) {
+__device__ __forceinline__ half8 frag(const Raw<T>& r, int s, uint32_t k0) {
     half8 o;
     if constexpr (T == kF16) {
-        o = r.v[j][s];
+        o = r.v[s];
     } else if constexpr (T == kF32) {
         for (int i = 0; i < 4; i++) {
-            o[i] = _Float16(r.v[j][s][0][i]);
-            o[i + 4] = _Float16(r.v[j][s][1][i]);
+            o[i] = _Float16(r.v[s][0][i]);
+            o[i + 4] = _Float16(r.v[s][1][i]);
         }
     } else if constexpr (T == kBF16) {
         for (int i = 0; i < 4; i++) {
-            o[2 * i] = _Float16(__uint_as_float(r.v[j][s][i] << 16));
-            o[2 * i + 1] = _Float16(__uint_as_float(r.v[j][s][i] & 0xFFFF0000u));
+            o[2 * i] = _Float16(__uint_as_float(r.v[s][i] << 16));
+            o[2 * i + 1] = _Float16(__uint_as_float(r.v[s][i] & 0xFFFF0000u));
         }
     } else if constexpr (T == kQ8_0) {
-        const float d = f16_bits(r.d[j]);
-        for (int i = 0; i < 8; i++) o[i] = _Float16(d * float(int8_t(byte_of(r.q[j][s][0], r.q[j][s][1], i))));
+        const float d = f16_bits(r.d);
+        for (int i = 0; i < 8; i++) o[i] = _Float16(d * float(int8_t(byte_of(r.q[s][0], r.q[s][1], i))));
     } else if constexpr (T == kQ4_0 || T == kQ4_1) {
-        const float d = f16_bits(r.d[j]);
+        const float d = f16_bits(r.d);
         float m = -8.f * d;
-        if constexpr (T == kQ4_1) m = f16_bits(r.m[j]);
+        if constexpr (T == kQ4_1) m = f16_bits(r.m);
         const int sh = 4 * s;  // elements 16..31 of the block are the high nibbles
-        for (int i = 0; i < 8; i++) o[i] = _Float16(d * float((byte_of(r.q[j][0], r.q[j][1], i) >> sh) & 0xF) + m);
+        for (int i = 0; i < 8; i++) o[i] = _Float16(d * float((byte_of(r.q[0], r.q[1], i) >> sh) & 0xF) + m);
     } else if constexpr (T == kQ6_K) {
         const uint32_t g = (k0 % 128) / 32;
-        const float sc = f16_bits(r.d[j]) * float(int8_t((r.sc[j] >> (8 * s)) & 0xFF));
+        const float sc = f16_bits(r.d) * float(int8_t((r.sc >> (8 * s)) & 0xFF));
         const int shl = g >= 2 ? 4 : 0, shh = 2 * int(g);
         for (int i = 0; i < 8; i++) {
-            const int q = int(((byte_of(r.ql[j][s][0], r.ql[j][s][1], i) >> shl) & 0xF) |
-                              (((byte_of(r.qh[j][s][0], r.qh[j][s][1], i) >> shh) & 3) << 4));
+            const int q = int(((byte_of(r.ql[s][0], r.ql[s][1], i) >> shl) & 0xF) |
+                              (((byte_of(r.qh[s][0], r.qh[s][1], i) >> shh) & 3) << 4));
             o[i] = _Float16(sc * float(q - 32));
         }
     }
     return o;
 }
 
+// Split-K bookkeeping: one counter per output tile (own 64-byte line), then the partial tiles.
+constexpr int kScDevice = 16;                 // buffer cache-policy bits: sc1 = device scope
+constexpr uint32_t kTileFloats = kMmToks * kMmRows;
+constexpr uint32_t kMaxSplits = 8;
+
 template <int T>
-__global__ __launch_bounds__(256) void linear_matmul_kernel(
+__global__ __launch_bounds__(512) void linear_matmul_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ out,
-    uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t row_bytes, uint32_t accumulate) {
+    uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t row_bytes, uint32_t accumulate,
+    uint32_t tiles_n, uint32_t tiles_m, uint32_t splits, uint32_t k_per_split, uint32_t per_xcd,
+    float* __restrict__ part, unsigned int* __restrict__ counters) {
+    // Register rings: W raw bytes DW steps ahead, x DX steps ahead of its LDS double buffer.
+    // A wait for the x of step t+1 (issued at step t+1-DX, before that step's W load) leaves
+    // every later load in flight, so both streams keep DX-1 or more steps of slack.
+    constexpr int DW = 4, DX = 4;
+    // Ring slots are indexed by the unrolled position d, equal to t mod DX and t mod 2 only
+    // when DW is a multiple of both.
+    static_assert(DW % DX == 0 && DW % 2 == 0, "ring depths");
     __shared__ __attribute__((aligned(16))) _Float16 xs[2][kMmToks * kXPitch];
     const uint32_t tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const uint32_t n = lane % 32, h = lane / 32;
-    const uint32_t tok0 = blockIdx.y * kMmToks;
-    const uint32_t rowbase = blockIdx.x * kMmRows + wave * kMmRowsWave;
 
-    // x staging: thread t converts 8 consecutive k of token t/4.
-    const uint32_t st_tok = tid / 4, st_k = 8 * (tid % 4);
-    const bool st_ok = tok0 + st_tok < n_tok;
-    const float* xrow = x + size_t(st_ok ? tok0 + st_tok : 0) * n_in + st_k;
-    float4v xa = {0.f, 0.f, 0.f, 0.f}, xb = xa;
-    auto load_x = [&](uint32_t k0) {
-        if (st_ok) {
-            xa = *reinterpret_cast<const float4v*>(xrow + k0);
-            xb = *reinterpret_cast<const float4v*>(xrow + k0 + 4);
-        }
+    // Workgroup b runs on XCD b % 8; give each XCD a contiguous run of (row tile, token tile,
+    // split) ids, split fastest, so the splits of a tile and the token tiles that share weight
+    // rows share one L2.
+    const uint32_t L = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    const uint32_t total = tiles_n * tiles_m * splits;
+    if (L >= total) return;
+    const uint32_t split = L % splits, tt = (L / splits) % tiles_m, rt = L / splits / tiles_m;
+    const uint32_t kbeg = split * k_per_split;
+    const uint32_t steps = (min(n_in, kbeg + k_per_split) - kbeg) / kMmK;
+    const uint32_t tok0 = tt * kMmToks;
+    const uint32_t rowbase = rt * kMmRows + wave * kMmRowsWave;
+
+    // x staging: thread t converts 4 consecutive k of token t/8. Loads are unconditional (rows
+    // past n_tok read the last token, steps past the split re-read its last step; neither
+    // reaches an output) so the rings stay in registers with exact wait counts.
+    const uint32_t st_tok = tid / 8, st_k = 4 * (tid % 8);
+    // A buffer load (wave-uniform descriptor over the workgroup's token rows, per-lane offset)
+    // keeps the compiler from moving these prefetches next to their use.
+    const uint32_t x_rows = min(n_tok - tok0, uint32_t(kMmToks));
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + size_t(tok0) * n_in), 0, int(4 * x_rows * n_in), kBufferFlags);
+    const uint32_t xoff = 4 * (min(st_tok, x_rows - 1) * n_in + kbeg + st_k);
+    float4v xr[DX];
+    auto load_x = [&](int slot, uint32_t t) {
+        xr[slot] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   xrs, int(xoff + 4 * min(t, steps - 1) * kMmK), 0, 0));
     };
-    auto store_x = [&](int buf) {
-        half8 v;
-        for (int i = 0; i < 4; i++) { v[i] = _Float16(xa[i]); v[i + 4] = _Float16(xb[i]); }
-        *reinterpret_cast<half8*>(&xs[buf][st_tok * kXPitch + st_k]) = v;
+    auto store_x = [&](int slot, int buf) {
+        typedef _Float16 half4_ __attribute__((ext_vector_type(4)));
+        const half4_ v = {_Float16(xr[slot][0]), _Float16(xr[slot][1]), _Float16(xr[slot][2]),
+                          _Float16(xr[slot][3])};
+        *reinterpret_cast<half4_*>(&xs[buf][st_tok * kXPitch + st_k]) = v;
     };
 
-    const uint8_t* rows[2];
-    for (int j = 0; j < 2; j++)
-        rows[j] = W + size_t(min(rowbase + 32 * j + n, n_out - 1)) * row_bytes;
+    const uint8_t* row = W + size_t(min(rowbase + n, n_out - 1)) * row_bytes;
+    const uint32_t k_last = kbeg + (steps - 1) * kMmK;
 
-    float16v_ acc[2][2];
+    float16v_ acc[2];
     for (int i = 0; i < 2; i++)
-        for (int j = 0; j < 2; j++)
-            for (int e = 0; e < 16; e++) acc[i][j][e] = 0.f;
+        for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
 
-    Raw<T> raw;
-    load_raw<T>(raw, rows, 0, h);
-    load_x(0);
-    store_x(0);
+#pragma unroll
+    for (int d = 0; d < DX; d++) load_x(d, d);
+    Raw<T> raw[DW];
+#pragma unroll
+    for (int d = 0; d < DW; d++) load_raw<T>(raw[d], row, min(kbeg + d * kMmK, k_last), h);
+    store_x(0, 0);
     __syncthreads();
 
-    const uint32_t steps = n_in / kMmK;
-    for (uint32_t t = 0; t < steps; t++) {
-        const uint32_t k0 = t * kMmK;
-        const int buf = t & 1;
-        half8 b[2][2];
-        for (int j = 0; j < 2; j++)
-            for (int s = 0; s < 2; s++) b[j][s] = frag<T>(raw, j, s, k0);
-        const bool more = t + 1 < steps;
-        if (more) {
-            load_raw<T>(raw, rows, k0 + kMmK, h);
-            load_x(k0 + kMmK);
-        }
+    for (uint32_t t0 = 0; t0 < steps; t0 += DW) {
 #pragma unroll
-        for (int s = 0; s < 2; s++) {
-            half8 a[2];
-            for (int i = 0; i < 2; i++)
-                a[i] = *reinterpret_cast<const half8*>(&xs[buf][(32 * i + n) * kXPitch + 16 * s + 8 * h]);
-            for (int i = 0; i < 2; i++)
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b[j][s], acc[i][j], 0, 0, 0);
+        for (int d = 0; d < DW; d++) {
+            const uint32_t t = t0 + d;
+            if (t >= steps) break;
+            const uint32_t k0 = kbeg + t * kMmK;
+            const int buf = d & 1;  // == t & 1 (DW is even)
+            load_x(d % DX, t + DX);  // the slot of step t, whose x is already in LDS
+            half8 b[2];
+            for (int s = 0; s < 2; s++) b[s] = frag<T>(raw[d], s, k0);
+            load_raw<T>(raw[d], row, min(k0 + DW * kMmK, k_last), h);
+#pragma unroll
+            for (int s = 0; s < 2; s++) {
+                for (int i = 0; i < 2; i++) {
+                    const half8 a = *reinterpret_cast<const half8*>(&xs[buf][(32 * i + n) * kXPitch + 16 * s + 8 * h]);
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[s], acc[i], 0, 0, 0);
+                }
+            }
+            store_x((d + 1) % DX, buf ^ 1);  // x of step t+1
+            __syncthreads();
         }
-        if (more) store_x(buf ^ 1);
-        __syncthreads();
     }
 
     // D[m][n] of a 32x32 tile: lane holds column n = lane%32, rows 8(e/4) + 4h + e%4.
-    for (int j = 0; j < 2; j++) {
-        const uint32_t row = rowbase + 32 * j + n;
-        if (row >= n_out) continue;
-        for (int i = 0; i < 2; i++) {
+    if (splits > 1) {
+        // Publish this split's partial tile (16-byte device-scope stores), count the arrival;
+        // the last split of the tile sums the partials in split order and writes the output.
+        const uint32_t tile = rt * tiles_m + tt;
+        const uint32_t tile_bytes = kTileFloats * 4;
+        const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+            part, 0, int(tiles_n * tiles_m * splits * tile_bytes), kBufferFlags);
+        auto off = [&](uint32_t sp, int i, int q) {
+            return int((tile * splits + sp) * tile_bytes + ((((wave * 2 + i) * 4 + q) * 64 + lane) * 16));
+        };
+        for (int i = 0; i < 2; i++)
+            for (int q = 0; q < 4; q++) {
+                const float4v v = {acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]};
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs, off(split, i, q), 0, kScDevice);
+            }
+        __builtin_amdgcn_s_waitcnt(0);  // the partial has reached device scope
+        __syncthreads();
+        __shared__ unsigned int last;
+        if (tid == 0) {
+            const unsigned prev = __hip_atomic_fetch_add(counters + tile * 16, 1u, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+            last = prev == splits - 1;
+        }
+        __syncthreads();
+        if (!last) return;
+        // Sum the partials in split order; all loads of a partial are issued together and the
+        // next partial's loads are in flight while the current one is added.
+        for (int i = 0; i < 2; i++)
+            for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
+        float4v pv[2][8];
+        auto load_part = [&](int slot, uint32_t sp) {
+            for (int i = 0; i < 2; i++)
+                for (int q = 0; q < 4; q++)
+                    pv[slot][i * 4 + q] = __builtin_bit_cast(
+                        float4v, __builtin_amdgcn_raw_buffer_load_b128(prs, off(sp, i, q), 0, kScDevice));
+        };
+        load_part(0, 0);
+        for (uint32_t sp = 0; sp < splits; sp += 2) {
+            load_part(1, min(sp + 1, splits - 1));
+            for (int i = 0; i < 2; i++)
+                for (int q = 0; q < 4; q++)
+                    for (int e = 0; e < 4; e++) acc[i][4 * q + e] += pv[0][i * 4 + q][e];
+            if (sp + 1 >= splits) break;
+            load_part(0, min(sp + 2, splits - 1));
+            for (int i = 0; i < 2; i++)
+                for (int q = 0; q < 4; q++)
+                    for (int e = 0; e < 4; e++) acc[i][4 * q + e] += pv[1][i * 4 + q][e];
+        }
+        if (tid == 0)  // leave the workspace ready for the next call
+            __hip_atomic_store(counters + tile * 16, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Output: all previous values are read before any store (the stores could alias later
+    // loads otherwise, which serializes every read-modify-write).
+    const uint32_t orow = rowbase + n;
+    if (orow < n_out) {
+        float prev[2][16];
+        for (int i = 0; i < 2; i++)
             for (int e = 0; e < 16; e++) {
                 const uint32_t tok = tok0 + 32 * i + 8 * (e / 4) + 4 * h + e % 4;
-                if (tok < n_tok) {
-                    float* o = out + size_t(tok) * n_out + row;
-                    *o = accumulate ? *o + acc[i][j][e] : acc[i][j][e];
-                }
+                prev[i][e] = accumulate && tok < n_tok ? out[size_t(tok) * n_out + orow] : 0.f;
             }
-        }
+        for (int i = 0; i < 2; i++)
+            for (int e = 0; e < 16; e++) {
+                const uint32_t tok = tok0 + 32 * i + 8 * (e / 4) + 4 * h + e % 4;
+                if (tok < n_tok) out[size_t(tok) * n_out + orow] = prev[i][e] + acc[i][e];
+            }
     }
 }
 
 template <int T>
 int launch_t(const uint8_t* W, const float* x, float* out, uint32_t n_in, uint32_t n_out,
-             uint32_t n_tok, uint32_t accumulate, hipStream_t stream) {
+             uint32_t n_tok, uint32_t accumulate, uint32_t n_splits, void* workspace,
+             size_t workspace_bytes, hipStream_t stream) {
     const uint32_t row_bytes = n_in / Fmt<T>::blk * Fmt<T>::bytes;
     if (n_tok == 1) {
         uint32_t r = kMvLdsRows / row_bytes;
@@ -387,27 +467,71 @@ int launch_t(const uint8_t* W, const float* x, float* out, uint32_t n_in, uint32
         hipLaunchKernelGGL(linear_matvec_kernel<T>, dim3(blocks), dim3(256), lds, stream, W, x, out,
                            n_in, n_out, r, row_bytes, uint64_t(n_out) * row_bytes, accumulate);
     } else {
-        const dim3 grid((n_out + kMmRows - 1) / kMmRows, (n_tok + kMmToks - 1) / kMmToks);
-        if (grid.y > 65535) return -1;
-        hipLaunchKernelGGL(linear_matmul_kernel<T>, grid, dim3(256), 0, stream, W, x, out, n_in,
-                           n_out, n_tok, row_bytes, accumulate);
+        const uint32_t tiles_n = (n_out + kMmRows - 1) / kMmRows;
+        const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
+        const uint32_t splits = workspace ? linear_splits(n_in, n_out, n_tok, n_splits, workspace_bytes) : 1;
+        const uint32_t steps = n_in / kMmK;
+        const uint32_t k_per_split = (steps + splits - 1) / splits * kMmK;
+        const uint64_t total = uint64_t(tiles_n) * tiles_m * splits;
+        const uint64_t per_xcd = (total + 7) / 8;
+        if (per_xcd * 8 > 0x7fffffffu) return -1;
+        auto* counters = static_cast<unsigned int*>(workspace);
+        auto* part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kLinearCounterBytes)
+                                : nullptr;
+        hipLaunchKernelGGL(linear_matmul_kernel<T>, dim3(uint32_t(per_xcd * 8)), dim3(kMmWaves * 64), 0, stream,
+                           W, x, out, n_in, n_out, n_tok, row_bytes, accumulate, tiles_n, tiles_m,
+                           splits, k_per_split, uint32_t(per_xcd), part, counters);
     }
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 }  // namespace
 
+uint32_t linear_splits(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested,
+                       size_t workspace_bytes) {
+    if (n_tok <= 1 || requested == 1) return 1;
+    const uint32_t tiles = ((n_out + kMmRows - 1) / kMmRows) * ((n_tok + kMmToks - 1) / kMmToks);
+    if (tiles > kLinearMaxTiles) return 1;
+    const uint32_t steps = n_in / kMmK;
+    // At least 8 k steps (256 elements) per split, at most kMaxSplits.
+    uint32_t cap = steps / 8;
+    if (cap > kMaxSplits) cap = kMaxSplits;
+    uint32_t s = 1;
+    if (requested > 1) {
+        s = requested < cap ? requested : cap;
+    } else {
+        // One workgroup per CU saturates a CU (a second co-resident one adds no throughput),
+        // and every split adds a partial tile to write and sum: take the largest split that
+        // still fits the tiles x splits workgroups on the 256 CUs in one round.
+        s = 256 / tiles;
+        if (s > cap) s = cap;
+    }
+    if (s < 2) return 1;
+    // No split may be empty.
+    const uint32_t per = (steps + s - 1) / s;
+    while (s > 1 && (s - 1) * per >= steps) s--;
+    if (kLinearCounterBytes + size_t(tiles) * s * kTileFloats * 4 > workspace_bytes) return 1;
+    return s;
+}
+
+size_t linear_workspace_size(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested) {
+    const uint32_t s = linear_splits(n_in, n_out, n_tok, requested, ~size_t(0));
+    const uint32_t tiles = ((n_out + kMmRows - 1) / kMmRows) * ((n_tok + kMmToks - 1) / kMmToks);
+    return kLinearCounterBytes + (s > 1 ? size_t(tiles) * s * kTileFloats * 4 : 0);
+}
+
 int launch_linear(uint32_t type, const void* W, const float* x, float* out, uint32_t n_in,
-                  uint32_t n_out, uint32_t n_tok, uint32_t accumulate, hipStream_t stream) {
+                  uint32_t n_out, uint32_t n_tok, uint32_t accumulate, uint32_t n_splits,
+                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
     const auto* w = static_cast<const uint8_t*>(W);
     switch (type) {
-        case kF32:  return launch_t<kF32>(w, x, out, n_in, n_out, n_tok, accumulate, stream);
-        case kF16:  return launch_t<kF16>(w, x, out, n_in, n_out, n_tok, accumulate, stream);
-        case kBF16: return launch_t<kBF16>(w, x, out, n_in, n_out, n_tok, accumulate, stream);
-        case kQ8_0: return launch_t<kQ8_0>(w, x, out, n_in, n_out, n_tok, accumulate, stream);
-        case kQ4_0: return launch_t<kQ4_0>(w, x, out, n_in, n_out, n_tok, accumulate, stream);
-        case kQ4_1: return launch_t<kQ4_1>(w, x, out, n_in, n_out, n_tok, accumulate, stream);
-        case kQ6_K: return launch_t<kQ6_K>(w, x, out, n_in, n_out, n_tok, accumulate, stream);
+        case kF32:  return launch_t<kF32>(w, x, out, n_in, n_out, n_tok, accumulate, n_splits, workspace, workspace_bytes, stream);
+        case kF16:  return launch_t<kF16>(w, x, out, n_in, n_out, n_tok, accumulate, n_splits, workspace, workspace_bytes, stream);
+        case kBF16: return launch_t<kBF16>(w, x, out, n_in, n_out, n_tok, accumulate, n_splits, workspace, workspace_bytes, stream);
+        case kQ8_0: return launch_t<kQ8_0>(w, x, out, n_in, n_out, n_tok, accumulate, n_splits, workspace, workspace_bytes, stream);
+        case kQ4_0: return launch_t<kQ4_0>(w, x, out, n_in, n_out, n_tok, accumulate, n_splits, workspace, workspace_bytes, stream);
+        case kQ4_1: return launch_t<kQ4_1>(w, x, out, n_in, n_out, n_tok, accumulate, n_splits, workspace, workspace_bytes, stream);
+        case kQ6_K: return launch_t<kQ6_K>(w, x, out, n_in, n_out, n_tok, accumulate, n_splits, workspace, workspace_bytes, stream);
         default: return -2;
     }
 }

@@ -29,6 +29,8 @@ EXPORTS = (
     "ingot_attn_strerror",
     "ingot_attn_version",
     "ingot_linear_weight_bytes",
+    "ingot_linear_splits",
+    "ingot_linear_workspace_size",
     "ingot_linear",
 )
 
@@ -93,6 +95,7 @@ class LinearDesc(ctypes.Structure):
         ("n_tok", c_uint32),
         ("out_offset", c_uint32),
         ("accumulate", c_uint32),
+        ("n_splits", c_uint32),
     ]
 
 
@@ -127,7 +130,11 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ingot_rope_kv_store.restype = c_int
     lib.ingot_linear_weight_bytes.argtypes = [ctypes.POINTER(LinearDesc)]
     lib.ingot_linear_weight_bytes.restype = c_size_t
-    lib.ingot_linear.argtypes = [c_void_p] * 3 + [ctypes.POINTER(LinearDesc), c_void_p]
+    lib.ingot_linear_splits.argtypes = [ctypes.POINTER(LinearDesc)]
+    lib.ingot_linear_splits.restype = c_uint32
+    lib.ingot_linear_workspace_size.argtypes = [ctypes.POINTER(LinearDesc)]
+    lib.ingot_linear_workspace_size.restype = c_size_t
+    lib.ingot_linear.argtypes = [c_void_p] * 4 + [c_size_t, ctypes.POINTER(LinearDesc), c_void_p]
     lib.ingot_linear.restype = c_int
     lib.ingot_attn_strerror.argtypes = [c_int]
     lib.ingot_attn_strerror.restype = ctypes.c_char_p
@@ -255,24 +262,41 @@ def rope_kv_store(q, k, v, k_cache, v_cache, inv_freq, desc: RopeKvDesc, stream=
     _check(rc, "ingot_rope_kv_store")
 
 
-def linear_desc(type_, n_in, n_out, n_tok=1, out_offset=0, accumulate=False):
+def linear_desc(type_, n_in, n_out, n_tok=1, out_offset=0, accumulate=False, n_splits=0):
     t = GGUF_TYPES[type_] if isinstance(type_, str) else int(type_)
-    return LinearDesc(t, n_in, n_out, n_tok, out_offset, 1 if accumulate else 0)
+    return LinearDesc(t, n_in, n_out, n_tok, out_offset, 1 if accumulate else 0, n_splits)
+
+
+def linear_splits(desc: LinearDesc) -> int:
+    return int(load_library().ingot_linear_splits(ctypes.byref(desc)))
 
 
 def linear_weight_bytes(desc: LinearDesc) -> int:
     return int(load_library().ingot_linear_weight_bytes(ctypes.byref(desc)))
 
 
-def linear(w, x, out, desc: LinearDesc, stream=None):
+def linear_workspace_size(desc: LinearDesc) -> int:
+    return int(load_library().ingot_linear_workspace_size(ctypes.byref(desc)))
+
+
+def linear(w, x, out, desc: LinearDesc, stream=None, workspace=None, use_workspace=True):
     """out[out_offset + t*n_out + r] (+)= W[r]·x[t] over the GGUF weight bytes `w`.
 
     w: uint8 CUDA tensor of the raw weight bytes (ingot_linear_weight_bytes long); x, out: f32
     CUDA tensors. Replaces encode_linear (src/metal_backend.mm:282-310); with accumulate it is
-    the wo projection plus residual add (src/metal_backend.mm:446-447).
+    the wo projection plus residual add (src/metal_backend.mm:446-447). The workspace (shared
+    per device by default) lets small batched calls split over n_in; use_workspace=False runs
+    without one.
     """
     lib = load_library()
+    ws, nws = None, 0
+    if use_workspace:
+        nbytes = lib.ingot_linear_workspace_size(ctypes.byref(desc))
+        if nbytes == 0:
+            _check(-1, "ingot_linear_workspace_size")
+        buf = (workspace or _workspace(x.device)).get(nbytes)
+        ws, nws = c_void_p(buf.data_ptr()), buf.numel()
     rc = lib.ingot_linear(c_void_p(w.data_ptr()), c_void_p(x.data_ptr()), c_void_p(out.data_ptr()),
-                          ctypes.byref(desc), _stream_ptr(stream))
+                          ws, c_size_t(nws), ctypes.byref(desc), _stream_ptr(stream))
     _check(rc, "ingot_linear")
     return out

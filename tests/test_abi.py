@@ -60,6 +60,7 @@ def test_struct_layout_matches_c():
     #include <stdio.h>
     #include <stddef.h>
     #include "ingot_attn.h"
+    #include "ingot_linear.h"
     int main(void) {
         printf("%zu %zu %zu %zu %zu\n", sizeof(IngotAttnDecodeDesc),
                offsetof(IngotAttnDecodeDesc, kv_offset), offsetof(IngotAttnDecodeDesc, scale),
@@ -68,6 +69,8 @@ def test_struct_layout_matches_c():
                offsetof(IngotAttnPrefillDesc, scale));
         printf("%zu %zu %zu %zu\n", sizeof(IngotRopeKvDesc), offsetof(IngotRopeKvDesc, dst_offset),
                offsetof(IngotRopeKvDesc, q_stride), offsetof(IngotRopeKvDesc, kv_stride));
+        printf("%zu %zu %zu\n", sizeof(IngotLinearDesc), offsetof(IngotLinearDesc, accumulate),
+               offsetof(IngotLinearDesc, n_splits));
         return 0;
     }
     """
@@ -78,9 +81,11 @@ def test_struct_layout_matches_c():
         subprocess.run(["gcc", "-I", INCLUDE, c, "-o", exe], check=True)
         vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True).stdout.split()]
     D, P, R = ingot_attn.DecodeDesc, ingot_attn.PrefillDesc, ingot_attn.RopeKvDesc
+    Li = ingot_attn.LinearDesc
     assert vals == [ctypes.sizeof(D), D.kv_offset.offset, D.scale.offset, ctypes.sizeof(P),
                     P.kv_offset.offset, P.q_stride.offset, P.scale.offset, ctypes.sizeof(R),
-                    R.dst_offset.offset, R.q_stride.offset, R.kv_stride.offset]
+                    R.dst_offset.offset, R.q_stride.offset, R.kv_stride.offset, ctypes.sizeof(Li),
+                    Li.accumulate.offset, Li.n_splits.offset]
 
 
 def test_host_validation(lib):
@@ -138,3 +143,39 @@ def test_rope_kv_store_validation(lib):
     assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 128, 0, 4, dst_offset=2)), None) == -1
     assert f(a, a, P((1 << 20) + 4), a, a, a, ctypes.byref(ok), None) == -1  # misaligned v
     assert f(a, a, a, a, a, a, ctypes.byref(ia.rope_kv_desc(24, 8, 128, 0xffffffff, 2)), None) == -1
+
+
+def test_linear_descriptor_checks(lib):
+    """Weight sizes per GGUF type, split resolution and argument checks of the linear layer
+    (no compute call)."""
+    import ingot_attn as ia
+
+    n = 3072
+    want = {"F32": 4 * n * n, "F16": 2 * n * n, "BF16": 2 * n * n, "Q8_0": n * n // 32 * 34,
+            "Q4_0": n * n // 32 * 18, "Q4_1": n * n // 32 * 20, "Q6_K": n * n // 256 * 210}
+    for t, nbytes in want.items():
+        assert ia.linear_weight_bytes(ia.linear_desc(t, n, n)) == nbytes
+    assert ia.linear_weight_bytes(ia.linear_desc(6, 256, 4)) == 0       # Q5_0: no kernel
+    assert ia.linear_weight_bytes(ia.linear_desc("Q6_K", 128, 4)) == 0  # n_in % 256
+    assert ia.linear_weight_bytes(ia.linear_desc("F16", 48, 4)) == 0    # n_in % 32
+    assert ia.linear_weight_bytes(ia.linear_desc("F16", 256, 4, n_splits=9)) == 0
+    # one token never splits; small batches split up to 8 ways, never into an empty split,
+    # and the workspace covers the chosen split
+    assert ia.linear_splits(ia.linear_desc("F16", n, n, 1)) == 1
+    for n_tok in (2, 64, 128, 256, 512, 1024, 4096):
+        d = ia.linear_desc("Q4_0", n, n, n_tok)
+        s = ia.linear_splits(d)
+        assert 1 <= s <= 8
+        tiles = -(-n // 256) * -(-n_tok // 64)
+        assert tiles * s <= max(256, tiles)
+        assert ia.linear_workspace_size(d) >= 16384 + (tiles * s * 64 * 256 * 4 if s > 1 else 0)
+    assert ia.linear_splits(ia.linear_desc("F16", 256, 256, 64, n_splits=8)) == 1  # 8 k steps min
+    assert ia.linear_splits(ia.linear_desc("F16", n, n, 64, n_splits=1)) == 1
+    assert ia.linear_splits(ia.linear_desc("F16", n, n, 64, n_splits=3)) == 3
+    P = ctypes.c_void_p
+    a = P(1 << 20)
+    d = ia.linear_desc("F16", 256, 4)
+    assert lib.ingot_linear(None, a, a, None, 0, ctypes.byref(d), None) == -1
+    assert lib.ingot_linear(P((1 << 20) + 8), a, a, None, 0, ctypes.byref(d), None) == -1  # w align
+    assert lib.ingot_linear(a, a, P((1 << 20) + 2), None, 0, ctypes.byref(d), None) == -1  # out align
+    assert lib.ingot_linear(a, a, a, None, 0, None, None) == -1

@@ -44,7 +44,7 @@ def _t(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-def _run(dev, t, raw, x, n_in, n_out, base=None, out_offset=0, pad=37):
+def _run(dev, t, raw, x, n_in, n_out, base=None, out_offset=0, pad=37, use_workspace=True):
     """Runs ingot_linear; returns (result [n_tok][n_out], the whole out buffer)."""
     import torch
     import ingot_attn as ia
@@ -57,7 +57,7 @@ def _run(dev, t, raw, x, n_in, n_out, base=None, out_offset=0, pad=37):
     out = _t(buf, dev)
     d = ia.linear_desc(t, n_in, n_out, n_tok, out_offset=out_offset, accumulate=base is not None)
     assert ia.linear_weight_bytes(d) == raw.size
-    ia.linear(_t(raw.reshape(-1), dev), _t(x, dev), out, d)
+    ia.linear(_t(raw.reshape(-1), dev), _t(x, dev), out, d, use_workspace=use_workspace)
     torch.cuda.synchronize()
     full = out.cpu().numpy()
     return full[out_offset:out_offset + n_tok * n_out].reshape(n_tok, n_out), full
@@ -133,12 +133,55 @@ def test_errors(dev):
     o = torch.zeros(256, dtype=torch.float32, device=dev)
     import ctypes
 
-    def call(d):
+    def call(d, ws=None):
         return lib.ingot_linear(ctypes.c_void_p(w.data_ptr()), ctypes.c_void_p(x.data_ptr()),
-                                ctypes.c_void_p(o.data_ptr()), ctypes.byref(d), None)
+                                ctypes.c_void_p(o.data_ptr()), ws, 0, ctypes.byref(d), None)
 
     assert call(ia.linear_desc(6, 256, 4)) == -2          # Q5_0: no kernel
     assert call(ia.linear_desc("Q6_K", 128, 4)) == -2     # n_in not a multiple of 256
     assert call(ia.linear_desc("F16", 0, 4)) == -1
     assert call(ia.linear_desc("F16", 256, 4)) == 0
+    assert call(ia.linear_desc("F16", 256, 4), ws=ctypes.c_void_p(o.data_ptr() + 4)) == -1  # misaligned
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("n_tok", [2, 64, 128, 512])
+def test_split_k_is_deterministic(dev, oracle_mod, n_tok):
+    """Small batches split n_in across workgroups (up to 8 ways); the result is the same on
+    every call (fixed-order partial sums, counters left at zero) and within f32 rounding of
+    the unsplit call; both match the f16-path oracle."""
+    import ingot_attn as ia
+
+    t, n = "Q4_0", 3072
+    d = ia.linear_desc(t, n, n, n_tok)
+    assert ia.linear_workspace_size(d) >= 16384
+    raw = gb.random_weights(t, n, n, seed=31)
+    x = _x(n_tok, n, seed=32)
+    a, _ = _run(dev, t, raw, x, n, n)
+    b, _ = _run(dev, t, raw, x, n, n)
+    c, _ = _run(dev, t, raw, x, n, n, use_workspace=False)
+    assert ia.linear_splits(d) > 1 or n_tok >= 512
+    np.testing.assert_array_equal(a, b)
+    _close(a, c, f"split vs unsplit n_tok={n_tok}")
+    _close(a, oracle_mod.linear(t, raw, x, n, n, f16_path=True), f"split n_tok={n_tok}")
+
+
+@pytest.mark.parametrize("n_splits", [2, 3, 5, 8])
+def test_requested_splits(dev, oracle_mod, n_splits):
+    """An explicit split count (uneven last split for 3 and 5 over 96 k steps) gives the same
+    result as no split, within f32 rounding, and matches the oracle."""
+    import torch
+    import ingot_attn as ia
+
+    t, n, n_tok = "Q8_0", 3072, 100
+    raw = gb.random_weights(t, n, n, seed=41)
+    x = _x(n_tok, n, seed=42)
+    d = ia.linear_desc(t, n, n, n_tok, n_splits=n_splits)
+    assert ia.linear_splits(d) == n_splits
+    out = _t(np.zeros((n_tok, n), np.float32), dev)
+    ia.linear(_t(raw.reshape(-1), dev), _t(x, dev), out, d)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref, _ = _run(dev, t, raw, x, n, n, use_workspace=False)
+    _close(got, ref, f"n_splits={n_splits} vs unsplit")
+    _close(got, oracle_mod.linear(t, raw, x, n, n, f16_path=True), f"n_splits={n_splits}")
