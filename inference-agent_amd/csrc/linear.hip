@@ -292,7 +292,18 @@ constexpr int kScDevice = 16;                 // buffer cache-policy bits: sc1 =
 constexpr uint32_t kTileFloats = kMmToks * kMmRows;
 constexpr uint32_t kMaxSplits = 8;
 
-template <int T>
+// W staged through LDS (LW kernels): a stage is `ks` elements of every row of the tile, `bytes`
+// per row (a whole number of 16-byte chunks, so lanes load full cache lines), stored at a row
+// pitch that keeps the B-operand reads free of bank conflicts. Types without an entry (Q8_0's
+// 34-byte and Q6_K's 210-byte blocks do not tile rows into 16-byte pieces) use the direct path.
+template <int T> struct Stage { static constexpr uint32_t ks = 0, bytes = 0, pitch = 0; };
+template <> struct Stage<kF32>  { static constexpr uint32_t ks = 32,  bytes = 128, pitch = 144; };
+template <> struct Stage<kF16>  { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 144; };
+template <> struct Stage<kBF16> { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 144; };
+template <> struct Stage<kQ4_0> { static constexpr uint32_t ks = 256, bytes = 144, pitch = 144; };
+template <> struct Stage<kQ4_1> { static constexpr uint32_t ks = 256, bytes = 160, pitch = 176; };
+
+template <int T, bool LW>
 __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ out,
     uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t row_bytes, uint32_t accumulate,
@@ -343,12 +354,88 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         *reinterpret_cast<half4_*>(&xs[buf][st_tok * kXPitch + st_k]) = v;
     };
 
-    const uint8_t* row = W + size_t(min(rowbase + n, n_out - 1)) * row_bytes;
-    const uint32_t k_last = kbeg + (steps - 1) * kMmK;
-
     float16v_ acc[2];
     for (int i = 0; i < 2; i++)
         for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
+
+    if constexpr (LW) {
+        // W through LDS: thread t loads 16-byte chunks t, t+512, ... of the stage (row-major,
+        // so 8-10 consecutive lanes cover one row's piece: whole cache lines), two stages ahead
+        // in registers; the chunks of stage j+1 are written to LDS buffer (j+1)&1 at the end of
+        // stage j. Each wave then builds its B operands from its 32 rows in LDS.
+        constexpr uint32_t KS = Stage<T>::ks, P = KS / kMmK, SB = Stage<T>::bytes;
+        constexpr uint32_t PITCH = Stage<T>::pitch, CH = SB / 16;
+        constexpr uint32_t NCH = (kMmRows * CH + 511) / 512;
+        constexpr uint32_t JU = P >= DX ? 2 : 2 * DX / P;  // stages per unrolled block
+        static_assert(KS % kMmK == 0 && (JU * P) % DX == 0, "stage shape");
+        extern __shared__ __attribute__((aligned(16))) uint8_t wsm[];  // [2][kMmRows][PITCH]
+        const uint32_t nst = steps / P;
+        const uint32_t rows_here = min(n_out - rt * kMmRows, uint32_t(kMmRows));
+        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(W + size_t(rt) * kMmRows * row_bytes), 0, int(rows_here * row_bytes),
+            kBufferFlags);
+        const uint32_t kbyte0 = kbeg / Fmt<T>::blk * Fmt<T>::bytes;
+        uint32_t goff[NCH], loff[NCH];
+        for (uint32_t i = 0; i < NCH; i++) {
+            const uint32_t c = min(tid + 512 * i, kMmRows * CH - 1);
+            const uint32_t r = c / CH, o = c % CH;
+            goff[i] = min(r, rows_here - 1) * row_bytes + kbyte0 + 16 * o;
+            loff[i] = r * PITCH + 16 * o;
+        }
+        u32x4 wr[2][NCH];
+        auto load_w = [&](int slot, uint32_t j) {
+            const uint32_t sb = min(j, nst - 1) * SB;
+            for (uint32_t i = 0; i < NCH; i++)
+                wr[slot][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                            wrs, int(goff[i] + sb), 0, 0));
+        };
+        auto store_w = [&](int slot) {
+            uint8_t* base = wsm + slot * (kMmRows * PITCH);
+            for (uint32_t i = 0; i < NCH; i++)
+                if (tid + 512 * i < kMmRows * CH) *reinterpret_cast<u32x4*>(base + loff[i]) = wr[slot][i];
+        };
+
+#pragma unroll
+        for (int d = 0; d < DX; d++) load_x(d, d);
+        load_w(0, 0);
+        load_w(1, 1);
+        store_x(0, 0);
+        store_w(0);
+        __syncthreads();
+
+        for (uint32_t j0 = 0; j0 < nst; j0 += JU) {
+#pragma unroll
+            for (uint32_t jj = 0; jj < JU; jj++) {
+                const uint32_t j = j0 + jj;
+                if (j >= nst) break;
+                const uint8_t* wrow = wsm + (jj & 1) * (kMmRows * PITCH) + (wave * kMmRowsWave + n) * PITCH;
+                load_w(jj & 1, j + 2);  // this slot's stage j is already in LDS
+#pragma unroll
+                for (uint32_t u = 0; u < P; u++) {
+                    const uint32_t t = j * P + u;
+                    const uint32_t d = jj * P + u;  // == t mod (JU*P): ring slots are compile-time
+                    const int buf = d & 1;
+                    load_x(d % DX, t + DX);
+                    Raw<T> r;
+                    load_raw<T>(r, wrow, u * kMmK, h);
+                    half8 b[2];
+                    for (int s = 0; s < 2; s++) b[s] = frag<T>(r, s, kbeg + t * kMmK);
+#pragma unroll
+                    for (int s = 0; s < 2; s++) {
+                        for (int i = 0; i < 2; i++) {
+                            const half8 a = *reinterpret_cast<const half8*>(&xs[buf][(32 * i + n) * kXPitch + 16 * s + 8 * h]);
+                            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[s], acc[i], 0, 0, 0);
+                        }
+                    }
+                    store_x((d + 1) % DX, buf ^ 1);  // x of step t+1
+                    if (u == P - 1) store_w((jj + 1) & 1);  // W of stage j+1
+                    __syncthreads();
+                }
+            }
+        }
+    } else {
+    const uint8_t* row = W + size_t(min(rowbase + n, n_out - 1)) * row_bytes;
+    const uint32_t k_last = kbeg + (steps - 1) * kMmK;
 
 #pragma unroll
     for (int d = 0; d < DX; d++) load_x(d, d);
@@ -379,6 +466,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
             store_x((d + 1) % DX, buf ^ 1);  // x of step t+1
             __syncthreads();
         }
+    }
     }
 
     // D[m][n] of a 32x32 tile: lane holds column n = lane%32, rows 8(e/4) + 4h + e%4.
@@ -469,18 +557,37 @@ int launch_t(const uint8_t* W, const float* x, float* out, uint32_t n_in, uint32
     } else {
         const uint32_t tiles_n = (n_out + kMmRows - 1) / kMmRows;
         const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
-        const uint32_t splits = workspace ? linear_splits(n_in, n_out, n_tok, n_splits, workspace_bytes) : 1;
-        const uint32_t steps = n_in / kMmK;
-        const uint32_t k_per_split = (steps + splits - 1) / splits * kMmK;
+        uint32_t splits = workspace ? linear_splits(n_in, n_out, n_tok, n_splits, workspace_bytes) : 1;
+        // LDS-staged W when rows split into whole 16-byte stage pieces.
+        constexpr uint32_t KS = Stage<T>::ks;
+        const bool lw = KS != 0 && row_bytes % 16 == 0 && n_in % KS == 0;
+        const uint32_t gran = lw ? KS : kMmK;
+        const uint32_t units = n_in / gran;
+        const uint32_t k_per_split = (units + splits - 1) / splits * gran;
+        splits = (n_in + k_per_split - 1) / k_per_split;  // never more than requested
         const uint64_t total = uint64_t(tiles_n) * tiles_m * splits;
         const uint64_t per_xcd = (total + 7) / 8;
         if (per_xcd * 8 > 0x7fffffffu) return -1;
         auto* counters = static_cast<unsigned int*>(workspace);
         auto* part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kLinearCounterBytes)
                                 : nullptr;
-        hipLaunchKernelGGL(linear_matmul_kernel<T>, dim3(uint32_t(per_xcd * 8)), dim3(kMmWaves * 64), 0, stream,
-                           W, x, out, n_in, n_out, n_tok, row_bytes, accumulate, tiles_n, tiles_m,
-                           splits, k_per_split, uint32_t(per_xcd), part, counters);
+        const dim3 grid(uint32_t(per_xcd * 8)), block(kMmWaves * 64);
+        if constexpr (Stage<T>::ks != 0) {
+            if (lw) {
+                const size_t lds = size_t(2) * kMmRows * Stage<T>::pitch;
+                static const hipError_t attr = hipFuncSetAttribute(
+                    reinterpret_cast<const void*>(&linear_matmul_kernel<T, true>),
+                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+                if (attr != hipSuccess) return -4;
+                hipLaunchKernelGGL((linear_matmul_kernel<T, true>), grid, block, lds, stream, W, x, out,
+                                   n_in, n_out, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits,
+                                   k_per_split, uint32_t(per_xcd), part, counters);
+                return hipGetLastError() == hipSuccess ? 0 : -4;
+            }
+        }
+        hipLaunchKernelGGL((linear_matmul_kernel<T, false>), grid, block, 0, stream, W, x, out, n_in,
+                           n_out, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits, k_per_split,
+                           uint32_t(per_xcd), part, counters);
     }
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
