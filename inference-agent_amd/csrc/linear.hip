@@ -268,10 +268,24 @@ __device__ __forceinline__ half8 frag(const Raw<T>& r, int s, uint32_t k0) {
     } else if constexpr (T == kQ8_0) {
         const float d = f16_bits(r.d);
         for (int i = 0; i < 8; i++) o[i] = _Float16(d * float(int8_t(byte_of(r.q[s][0], r.q[s][1], i))));
-    } else if constexpr (T == kQ4_0 || T == kQ4_1) {
+    } else if constexpr (T == kQ4_0) {
+        // Packed f16: the nibble n becomes the half 1024 + n (bits 0x6400 | n), minus 1032 gives
+        // n - 8 exactly, times d rounds once — the same value as d*(n-8) formed in f32 and
+        // rounded to half.
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const _Float16 dh = __builtin_bit_cast(_Float16, uint16_t(r.d));
+        const h2 dd = {dh, dh}, off = {_Float16(-1032.f), _Float16(-1032.f)};
+        const uint32_t sh = 4 * s;  // elements 16..31 of the block are the high nibbles
+        for (int p = 0; p < 4; p++) {
+            // bytes 2p, 2p+1 into the low byte of each half
+            const uint32_t v = __builtin_amdgcn_perm(0u, p < 2 ? r.q[0] : r.q[1], (p & 1) ? 0x0c030c02u : 0x0c010c00u);
+            const h2 hv = (__builtin_bit_cast(h2, ((v >> sh) & 0x000F000Fu) | 0x64006400u) + off) * dd;
+            o[2 * p] = hv[0];
+            o[2 * p + 1] = hv[1];
+        }
+    } else if constexpr (T == kQ4_1) {
         const float d = f16_bits(r.d);
-        float m = -8.f * d;
-        if constexpr (T == kQ4_1) m = f16_bits(r.m);
+        const float m = f16_bits(r.m);
         const int sh = 4 * s;  // elements 16..31 of the block are the high nibbles
         for (int i = 0; i < 8; i++) o[i] = _Float16(d * float((byte_of(r.q[0], r.q[1], i) >> sh) & 0xF) + m);
     } else if constexpr (T == kQ6_K) {
@@ -294,12 +308,13 @@ constexpr uint32_t kMaxSplits = 8;
 
 // W staged through LDS (LW kernels): a stage is `ks` elements of every row of the tile, `bytes`
 // per row (a whole number of 16-byte chunks, so lanes load full cache lines), stored at a row
-// pitch that keeps the B-operand reads free of bank conflicts. Types without an entry (Q8_0's
-// 34-byte and Q6_K's 210-byte blocks do not tile rows into 16-byte pieces) use the direct path.
+// pitch that keeps the B-operand reads free of bank conflicts. Q6_K has no entry (its 210-byte
+// blocks do not tile rows into 16-byte pieces of a size that fits): it uses the direct path.
 template <int T> struct Stage { static constexpr uint32_t ks = 0, bytes = 0, pitch = 0; };
 template <> struct Stage<kF32>  { static constexpr uint32_t ks = 32,  bytes = 128, pitch = 144; };
 template <> struct Stage<kF16>  { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 144; };
 template <> struct Stage<kBF16> { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 144; };
+template <> struct Stage<kQ8_0> { static constexpr uint32_t ks = 256, bytes = 272, pitch = 272; };
 template <> struct Stage<kQ4_0> { static constexpr uint32_t ks = 256, bytes = 144, pitch = 144; };
 template <> struct Stage<kQ4_1> { static constexpr uint32_t ks = 256, bytes = 160, pitch = 176; };
 
