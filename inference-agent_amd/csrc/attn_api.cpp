@@ -10,6 +10,7 @@
 
 #include "../../include/ingot_attn.h"
 #include "../../include/ingot_linear.h"
+#include "../../include/ingot_model.h"
 #include "attn_internal.h"
 
 namespace {
@@ -176,6 +177,35 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
                                           d->n_head_kv, d->n_head / d->n_head_kv, splits, d->scale,
                                           static_cast<hipStream_t>(stream));
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+}
+
+int ingot_rmsnorm(const float* x, const float* w, float* out, uint32_t n, uint32_t n_rows, float eps,
+                  void* stream) {
+    if (!x || !w || !out || n == 0 || n_rows == 0 || n % 4 != 0) return INGOT_ATTN_EINVAL;
+    if (!aligned16(x) || !aligned16(w) || !aligned16(out) || !(eps >= 0.f)) return INGOT_ATTN_EINVAL;
+    if (n_rows > 0x7fffffffu) return INGOT_ATTN_EINVAL;
+    return ingot::launch_rmsnorm(x, w, out, n, n_rows, eps, static_cast<hipStream_t>(stream)) == 0
+               ? INGOT_ATTN_OK : INGOT_ATTN_EHIP;
+}
+
+int ingot_silu_mul(float* gate, const float* up, uint64_t n, void* stream) {
+    if (!gate || !up || n == 0 || n % 4 != 0 || !aligned16(gate) || !aligned16(up)) return INGOT_ATTN_EINVAL;
+    const int rc = ingot::launch_silu_mul(gate, up, n, static_cast<hipStream_t>(stream));
+    return rc == 0 ? INGOT_ATTN_OK : rc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
+}
+
+int ingot_get_rows(uint32_t type, const void* w, uint32_t n, uint32_t n_rows, const int32_t* tokens,
+                   uint32_t n_tok, float* out, void* stream) {
+    if (!w || !tokens || !out || n == 0 || n_rows == 0 || n_tok == 0 || n_tok > 0x7fffffffu)
+        return INGOT_ATTN_EINVAL;
+    uint32_t elems, bytes;
+    linear_block(type, elems, bytes);
+    if (elems == 0 || n % elems != 0) return INGOT_ATTN_EUNSUPPORTED;
+    if ((reinterpret_cast<uintptr_t>(w) & 3u) != 0 || (reinterpret_cast<uintptr_t>(out) & 3u) != 0)
+        return INGOT_ATTN_EINVAL;
+    return ingot::launch_get_rows(type, w, uint64_t(n / elems) * bytes, n, n_rows, tokens, n_tok, out,
+                                  static_cast<hipStream_t>(stream)) == 0
+               ? INGOT_ATTN_OK : INGOT_ATTN_EHIP;
 }
 
 int ingot_rope_kv_store(float* q, const float* k, const float* v, uint16_t* k_cache,

@@ -50,4 +50,11 @@ uint32_t linear_splits(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t r
                        size_t workspace_bytes);
 size_t linear_workspace_size(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested);
 
+// Per-layer model ops (model_ops.hip). Return 0, -1 (grid too large) or -4 (launch failed).
+int launch_rmsnorm(const float* x, const float* w, float* out, uint32_t n, uint32_t n_rows, float eps,
+                   hipStream_t stream);
+int launch_silu_mul(float* gate, const float* up, uint64_t n, hipStream_t stream);
+int launch_get_rows(uint32_t type, const void* w, uint64_t row_bytes, uint32_t n, uint32_t n_rows,
+                    const int32_t* tokens, uint32_t n_tok, float* out, hipStream_t stream);
+
 }  // namespace ingot

@@ -32,6 +32,9 @@ EXPORTS = (
     "ingot_linear_splits",
     "ingot_linear_workspace_size",
     "ingot_linear",
+    "ingot_rmsnorm",
+    "ingot_silu_mul",
+    "ingot_get_rows",
 )
 
 # GGUF tensor type ids (ggml's enum, src/gguf.h:30-33) with a linear kernel, and their
@@ -136,6 +139,13 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ingot_linear_workspace_size.restype = c_size_t
     lib.ingot_linear.argtypes = [c_void_p] * 4 + [c_size_t, ctypes.POINTER(LinearDesc), c_void_p]
     lib.ingot_linear.restype = c_int
+    lib.ingot_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_float, c_void_p]
+    lib.ingot_rmsnorm.restype = c_int
+    lib.ingot_silu_mul.argtypes = [c_void_p, c_void_p, c_uint64, c_void_p]
+    lib.ingot_silu_mul.restype = c_int
+    lib.ingot_get_rows.argtypes = [c_uint32, c_void_p, c_uint32, c_uint32, c_void_p, c_uint32, c_void_p,
+                                   c_void_p]
+    lib.ingot_get_rows.restype = c_int
     lib.ingot_attn_strerror.argtypes = [c_int]
     lib.ingot_attn_strerror.restype = ctypes.c_char_p
     lib.ingot_attn_version.argtypes = []
@@ -299,4 +309,29 @@ def linear(w, x, out, desc: LinearDesc, stream=None, workspace=None, use_workspa
     rc = lib.ingot_linear(c_void_p(w.data_ptr()), c_void_p(x.data_ptr()), c_void_p(out.data_ptr()),
                           ws, c_size_t(nws), ctypes.byref(desc), _stream_ptr(stream))
     _check(rc, "ingot_linear")
+    return out
+
+
+def rmsnorm(x, w, out, n, n_rows, eps, stream=None):
+    """out = rmsnorm(x) * w per row (include/ingot_model.h; encode_rmsnorm)."""
+    rc = load_library().ingot_rmsnorm(c_void_p(x.data_ptr()), c_void_p(w.data_ptr()), c_void_p(out.data_ptr()),
+                                      n, n_rows, c_float(eps), _stream_ptr(stream))
+    _check(rc, "ingot_rmsnorm")
+    return out
+
+
+def silu_mul(gate, up, n, stream=None):
+    """gate = silu(gate) * up (encode_silu_mul)."""
+    rc = load_library().ingot_silu_mul(c_void_p(gate.data_ptr()), c_void_p(up.data_ptr()), n,
+                                       _stream_ptr(stream))
+    _check(rc, "ingot_silu_mul")
+    return gate
+
+
+def get_rows(type_, w, n, n_rows, tokens, n_tok, out, stream=None):
+    """out[t] = dequantized row tokens[t] of the GGUF table w (tokens: int32 CUDA tensor)."""
+    t = GGUF_TYPES[type_] if isinstance(type_, str) else int(type_)
+    rc = load_library().ingot_get_rows(t, c_void_p(w.data_ptr()), n, n_rows, c_void_p(tokens.data_ptr()),
+                                       n_tok, c_void_p(out.data_ptr()), _stream_ptr(stream))
+    _check(rc, "ingot_get_rows")
     return out

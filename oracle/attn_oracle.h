@@ -47,6 +47,35 @@ int oracle_linear(int type, const uint8_t* w, const float* x, float* out, int n_
 int oracle_linear_f16(int type, const uint8_t* w, const float* x, float* out, int n_in, int n_out,
                       int n_tok, int accumulate, int n_threads);
 
+// Model-level pieces (model_oracle.cpp).
+void oracle_rmsnorm(const float* x, const float* w, float* out, int n, int n_rows, float eps);
+void oracle_silu_mul(float* gate, const float* up, size_t n);
+
+typedef struct OracleTensor {
+    int type;          // GGUF type id
+    const void* data;  // the tensor's bytes (GGUF layout)
+} OracleTensor;
+
+typedef struct OracleLayer {
+    const float* attn_norm;
+    const float* ffn_norm;
+    OracleTensor wq, wk, wv, wo, w_gate, w_up, w_down;
+} OracleLayer;
+
+typedef struct OracleModel {
+    int n_layer, n_embd, n_head, n_head_kv, head_dim, n_ff, n_vocab;
+    float rms_eps;
+    const float* rope_inv_freq;  // head_dim/2
+    OracleTensor tok_embd, output;
+    const float* output_norm;
+    const OracleLayer* layers;   // n_layer
+} OracleModel;
+
+// CpuBackend::forward for one token at pos (0 <= pos < n_ctx): writes K/V (f16) into the cache
+// rows of pos and the logits [n_vocab]. f16_linear selects the Metal batched linear numerics.
+int oracle_forward(const OracleModel* m, uint16_t* k_cache, uint16_t* v_cache, int n_ctx, int token,
+                   int pos, float* logits, int f16_linear, int n_threads);
+
 #ifdef __cplusplus
 }
 #endif

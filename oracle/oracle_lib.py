@@ -37,6 +37,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_rope_kv_store.argtypes = ([c_void_p, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p,
                                             c_void_p, c_size_t] + [c_int] * 4 + [c_void_p])
         L.oracle_rope_kv_store.restype = c_int
+        L.oracle_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_int, c_float]
+        L.oracle_silu_mul.argtypes = [c_void_p, c_void_p, c_size_t]
         L.oracle_dequant_row.argtypes = [c_int, c_void_p, c_void_p, c_int]
         L.oracle_dequant_row.restype = c_int
         for f in (L.oracle_linear, L.oracle_linear_f16):
@@ -178,3 +180,84 @@ def linear(type_, w: np.ndarray, x: np.ndarray, n_in: int, n_out: int, out=None,
     if rc != 0:
         raise ValueError("oracle_linear: bad argument")
     return out
+
+
+# ---------------------------------------------------------------- model-level oracle
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    """ops::rmsnorm per row (src/ops.cpp:226-231)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    out = np.empty_like(x)
+    lib().oracle_rmsnorm(_ptr(x), _ptr(np.ascontiguousarray(w, dtype=np.float32)), _ptr(out), n,
+                         x.size // n, c_float(eps))
+    return out
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """silu(gate) * up (src/cpu_backend.cpp:77, src/ops.h:35)."""
+    g = np.ascontiguousarray(gate, dtype=np.float32).copy()
+    lib().oracle_silu_mul(_ptr(g), _ptr(np.ascontiguousarray(up, dtype=np.float32)), g.size)
+    return g
+
+
+class _Tensor(ctypes.Structure):
+    _fields_ = [("type", c_int), ("data", c_void_p)]
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [("attn_norm", c_void_p), ("ffn_norm", c_void_p)] + [
+        (n, _Tensor) for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down")]
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [(n, c_int) for n in ("n_layer", "n_embd", "n_head", "n_head_kv", "head_dim", "n_ff",
+                                     "n_vocab")] + [
+        ("rms_eps", c_float), ("rope_inv_freq", c_void_p), ("tok_embd", _Tensor), ("output", _Tensor),
+        ("output_norm", c_void_p), ("layers", ctypes.POINTER(_Layer))]
+
+
+class ForwardOracle:
+    """CpuBackend::forward (src/cpu_backend.cpp:22-90) over a model given as numpy arrays, with an
+    f16 KV cache; `forward(token, pos, f16_linear)` returns the logits."""
+
+    def __init__(self, model, n_ctx: int, threads=None):
+        self.m = model
+        c = model["cfg"]
+        self.n_ctx = n_ctx
+        self.threads = threads or min(8, os.cpu_count() or 1)
+        self._keep = []
+
+        def arr(a, dt):
+            a = np.ascontiguousarray(a, dtype=dt)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        def ten(t):
+            return _Tensor(_type_id(t[0]), arr(t[1], np.uint8))
+
+        layers = (_Layer * c["n_layer"])()
+        for l, L in enumerate(model["layers"]):
+            layers[l].attn_norm = arr(L["attn_norm"], np.float32)
+            layers[l].ffn_norm = arr(L["ffn_norm"], np.float32)
+            for n in ("wq", "wk", "wv", "wo", "w_gate", "w_up", "w_down"):
+                setattr(layers[l], n, ten(L[n]))
+        self._layers = layers
+        self.model = _Model(c["n_layer"], c["n_embd"], c["n_head"], c["n_head_kv"], c["head_dim"], c["n_ff"],
+                            c["n_vocab"], c["rms_eps"], arr(model["rope_inv_freq"], np.float32),
+                            ten(model["tok_embd"]), ten(model["output"]), arr(model["output_norm"], np.float32),
+                            layers)
+        kv_dim = c["n_head_kv"] * c["head_dim"]
+        self.k_cache = np.zeros((c["n_layer"], n_ctx, kv_dim), dtype=np.uint16)
+        self.v_cache = np.zeros_like(self.k_cache)
+        lib().oracle_forward.argtypes = [ctypes.POINTER(_Model), c_void_p, c_void_p, c_int, c_int, c_int,
+                                         c_void_p, c_int, c_int]
+        lib().oracle_forward.restype = c_int
+
+    def forward(self, token: int, pos: int, f16_linear: bool = False) -> np.ndarray:
+        logits = np.empty(self.m["cfg"]["n_vocab"], dtype=np.float32)
+        rc = lib().oracle_forward(ctypes.byref(self.model), _ptr(self.k_cache), _ptr(self.v_cache),
+                                  self.n_ctx, token, pos, _ptr(logits), 1 if f16_linear else 0, self.threads)
+        if rc != 0:
+            raise ValueError("oracle_forward: bad argument")
+        return logits

@@ -1,0 +1,164 @@
+"""GPU parity of the per-layer model ops and of the whole Llama forward pass (ingot_forward,
+built only on the C ABI) against the CPU oracle.
+
+Tolerances, stated per output:
+  - rmsnorm: |d| <= 2e-6 * (1 + |ref|) (f32, a tree sum instead of a left-to-right one);
+  - silu_mul: |d| <= 2e-6 * (1 + |ref|) (the GPU's expf vs the host's);
+  - get_rows: bit-exact (each value is one f16 widening, or d times a small integer, exact in
+    f32, except Q6_K's d*scale*q, two roundings in the same order on both sides);
+  - forward, decode steps (n_tok = 1: f32 matvecs, decode attention): logits within rel-L2 1e-4
+    of the oracle's f32 forward;
+  - forward, a prefill chunk (batched: x and weights rounded to f16 in every projection, f16
+    Q·scale and P in the prefill attention — the reference's Metal numerics): logits within
+    rel-L2 5e-3 of the oracle's forward with the f16 projections (oracle_linear_f16), and the
+    K/V cache rows within 1e-2 relative; the decode steps that follow stay within 5e-3.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import ensure_built
+
+import gguf_blocks as gb
+import llama_synth as ls
+
+pytestmark = pytest.mark.gpu
+
+CFG = dict(n_layer=2, n_embd=512, n_head=4, n_head_kv=2, head_dim=128, n_ff=1024, n_vocab=1000,
+           rope_theta=500000.0, rms_eps=1e-5)
+MIXED = {"embd": "Q8_0", "wq": "Q4_0", "wk": "Q4_1", "wv": "Q8_0", "wo": "Q4_0", "w_gate": "Q6_K",
+         "w_up": "F16", "w_down": "Q4_0", "output": "Q6_K"}
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a GPU")
+    ensure_built("lib")
+    import ingot_attn
+
+    ingot_attn.load_library()
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def test_rmsnorm(dev, oracle_mod):
+    import torch
+    import ingot_attn as ia
+
+    rng = np.random.default_rng(1)
+    for n, rows in ((3072, 1), (3072, 37), (512, 4), (8192, 2)):
+        x = rng.standard_normal((rows, n)).astype(np.float32) * 3
+        w = rng.standard_normal(n).astype(np.float32)
+        out = torch.empty(rows, n, dtype=torch.float32, device=dev)
+        ia.rmsnorm(_t(x, dev), _t(w, dev), out, n, rows, 1e-5)
+        torch.cuda.synchronize()
+        want = oracle_mod.rmsnorm(x, w, 1e-5)
+        assert np.all(np.abs(out.cpu().numpy() - want) <= 2e-6 * (1 + np.abs(want)))
+    # in place
+    xd = _t(x, dev)
+    ia.rmsnorm(xd, _t(w, dev), xd, n, rows, 1e-5)
+    torch.cuda.synchronize()
+    assert np.all(np.abs(xd.cpu().numpy() - want) <= 2e-6 * (1 + np.abs(want)))
+
+
+def test_silu_mul(dev, oracle_mod):
+    import torch
+    import ingot_attn as ia
+
+    rng = np.random.default_rng(2)
+    g = (rng.standard_normal(8192 * 5) * 4).astype(np.float32)
+    u = rng.standard_normal(8192 * 5).astype(np.float32)
+    gd = _t(g, dev)
+    ia.silu_mul(gd, _t(u, dev), g.size)
+    torch.cuda.synchronize()
+    want = oracle_mod.silu_mul(g, u)
+    assert np.all(np.abs(gd.cpu().numpy() - want) <= 2e-6 * (1 + np.abs(want)))
+
+
+@pytest.mark.parametrize("t", ["F32", "F16", "BF16", "Q8_0", "Q4_0", "Q4_1", "Q6_K"])
+def test_get_rows(dev, oracle_mod, t):
+    import torch
+    import ingot_attn as ia
+
+    n, rows = 512, 300
+    raw = gb.random_weights(t, rows, n, seed=5)
+    ids = np.array([0, 299, 17, 17, 150, -1, 300], np.int32)  # the last two are out of range
+    out = torch.full((len(ids), n), float("nan"), dtype=torch.float32, device=dev)
+    ia.get_rows(t, _t(raw.reshape(-1), dev), n, rows, _t(ids, dev), len(ids), out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    table = oracle_mod.dequant_rows(t, raw, n)
+    np.testing.assert_array_equal(got[:5], table[ids[:5]])
+    assert np.all(got[5:] == 0.0)
+
+
+def _run(dev, oracle_mod, types, prefill, decode_steps, tied):
+    import torch
+    from ingot_forward import HipForward
+
+    m = ls.make_model(CFG, types, seed=7, tied=tied)
+    n_ctx = 128
+    gpu = HipForward(m, n_ctx=n_ctx, n_batch=64, device=dev)
+    orc = oracle_mod.ForwardOracle(m, n_ctx=n_ctx)
+    rng = np.random.default_rng(8)
+    toks = rng.integers(0, CFG["n_vocab"], prefill + decode_steps).tolist()
+    res = []
+    g = gpu.forward_batch(toks[:prefill], 0).cpu().numpy()
+    want = None
+    for p in range(prefill):
+        want = orc.forward(toks[p], p, f16_linear=prefill > 1)
+    res.append(("prefill", g, want))
+    # cache rows written by the chunk
+    kv = CFG["n_head_kv"] * CFG["head_dim"]
+    kc = gpu.k_cache.view(torch.int16).cpu().numpy().view(np.uint16).reshape(CFG["n_layer"], n_ctx, kv)
+    for p in range(decode_steps):
+        pos = prefill + p
+        g = gpu.forward(toks[pos], pos).cpu().numpy()
+        res.append(("decode", g, orc.forward(toks[pos], pos)))
+    return res, kc[:, :prefill], orc.k_cache[:, :prefill]
+
+
+def _rel(a, b):
+    return float(np.linalg.norm(a.astype(np.float64) - b) / np.linalg.norm(b))
+
+
+@pytest.mark.parametrize("types,tied", [("F16", True), ("Q4_0", False), (MIXED, False)])
+def test_forward_decode_only(dev, oracle_mod, types, tied):
+    """Token-by-token from position 0: every step is the n_tok = 1 path."""
+    res, _, _ = _run(dev, oracle_mod, types, prefill=1, decode_steps=6, tied=tied)
+    for what, g, w in res:
+        assert np.all(np.isfinite(g))
+        assert _rel(g, w) <= 1e-4, (what, _rel(g, w))
+
+
+@pytest.mark.parametrize("types,prefill", [("F16", 37), ("Q4_0", 64), (MIXED, 50)])
+def test_forward_prefill_then_decode(dev, oracle_mod, types, prefill):
+    res, kc_gpu, kc_orc = _run(dev, oracle_mod, types, prefill=prefill, decode_steps=3, tied=True)
+    for what, g, w in res:
+        assert np.all(np.isfinite(g))
+        assert _rel(g, w) <= 5e-3, (what, _rel(g, w))
+    a = kc_gpu.view(np.float16).astype(np.float64)
+    b = kc_orc.view(np.float16).astype(np.float64)
+    assert np.linalg.norm(a - b) / np.linalg.norm(b) <= 1e-2
+
+
+def test_forward_errors(dev):
+    from ingot_forward import HipForward
+
+    m = ls.make_model(dict(CFG, n_layer=1), "F16", seed=9)
+    gpu = HipForward(m, n_ctx=16, n_batch=8, device=dev)
+    with pytest.raises(RuntimeError, match="batch size out of range"):
+        gpu.forward_batch(list(range(9)), 0)
+    with pytest.raises(RuntimeError, match="context window exceeded"):
+        gpu.forward_batch([1, 2], 15)
+    with pytest.raises(RuntimeError, match="token id out of range"):
+        gpu.forward_batch([1, 1000], 0)
