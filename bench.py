@@ -20,7 +20,8 @@ The same line carries the prefill figures (C4, C5-prefill, C2: TFLOPS and fracti
 f16-MFMA and HBM peaks), the decode sweep (C1, C5 lengths), the fused RoPE + KV-cache store
 that precedes attention (GB/s for a 512-token chunk and one decode token), the attention output
 projection wo with its residual add (GB/s for one token, TFLOPS for a 512-token chunk, four
-GGUF weight types) and the CPU baseline
+GGUF weight types), the whole Llama-3.2-3B forward pass with Q4_0 weights (decode tok/s at
+position 128, 512-token prefill tok/s; llama-bench's tg/pp measures) and the CPU baseline
 (the oracle, a C++ restatement of Ingot's CPU attention, on the host cores).
 """
 from __future__ import annotations
@@ -52,6 +53,9 @@ PREFILL = {"c4": "C4-prefill-512@3584", "c5p": "C5-prefill-2048@6144", "c2": "C2
 LINEAR = {"wo1-f16": ("F16", 1), "wo1-q8": ("Q8_0", 1), "wo1-q4": ("Q4_0", 1), "wo1-q6k": ("Q6_K", 1),
           "wo512-f16": ("F16", 512), "wo512-q8": ("Q8_0", 512), "wo512-q4": ("Q4_0", 512),
           "wo512-q6k": ("Q6_K", 512)}
+# name -> weight type: the whole Llama-3.2-3B forward pass (28 layers, tied embeddings) with
+# random-byte weights, one decode token at position 128 and a 512-token prefill chunk at 0
+MODEL = {"model-q4": "Q4_0"}
 # name -> (pos, n_tok): the KV-store step before attention, for a prefill chunk and a decode token
 KVSTORE = {"kv512": ("kv-store-512@3584", 3584, 512), "kv1": ("kv-store-1@4095", 4095, 1)}
 
@@ -182,6 +186,25 @@ class LinearBench:
             self.ia.linear(self.w[i], self.x, self.out, self.desc)
 
 
+class ModelBench:
+    """ingot_forward.HipForward (every step a libingot_attn.so call) over a full-size synthetic
+    Llama-3.2-3B; a step is one forward_batch (n tokens at `pos`), tokens already on the device."""
+
+    def __init__(self, torch, t, n_tok, pos, n_ctx=1024):
+        import llama_synth as ls
+        from ingot_forward import HipForward
+
+        self.model = ls.make_bench_model(ls.LLAMA32_3B, t, seed=5)
+        self.weight_bytes = ls.weight_bytes(self.model)
+        self.fw = HipForward(self.model, n_ctx=n_ctx, n_batch=max(n_tok, 1))
+        self.n_tok, self.pos = n_tok, pos
+        self.toks = list(range(1, n_tok + 1))
+        self.dev_toks = torch.tensor(self.toks, dtype=torch.int32, device=self.fw.dev)
+
+    def step(self):
+        self.fw.forward_batch(self.toks, self.pos, tokens_on_device=self.dev_toks)
+
+
 def time_steps(torch, fn, steps, warmup, use_graph):
     """Seconds per step over `steps` timed steps (after `warmup`), graph-replayed by default."""
     stream = torch.cuda.current_stream()
@@ -252,7 +275,7 @@ def main():
     use_graph = not args.no_graph
     sel = args.only
     want = lambda key, group: sel in ("all", group, key)
-    res = {"decode": {}, "prefill": {}, "kv_store": {}, "linear": {}}
+    res = {"decode": {}, "prefill": {}, "kv_store": {}, "linear": {}, "model": {}}
 
     head = None
     for key, (name, n_keys, kv_scale, seed) in DECODE.items():
@@ -319,6 +342,23 @@ def main():
             "flops_per_call": b.flops}
         del b
         torch.cuda.empty_cache()
+
+    for key, t in MODEL.items():
+        if not want(key, "model"):
+            continue
+        entry = {}
+        for phase, n_tok, pos in (("decode", 1, 128), ("prefill", 512, 0)):
+            b = ModelBench(torch, t, n_tok, pos)
+            steps = max(5, args.steps // 5)
+            sps = time_steps(torch, b.step, steps, args.warmup, use_graph)
+            entry[f"{phase}_ms"] = round(sps * 1e3, 3)
+            entry[f"{phase}_tok_s"] = round(n_tok / sps, 1)
+            if phase == "decode":
+                entry["decode_weight_GB/s"] = round(b.weight_bytes / sps / 1e9, 1)
+            entry["weight_bytes"] = b.weight_bytes
+            del b
+            torch.cuda.empty_cache()
+        res["model"][f"Llama-3.2-3B-{t}"] = entry
 
     cpu = None if args.no_cpu else cpu_baseline(W, args.cpu_seconds)
 

@@ -57,3 +57,61 @@ def make_model(cfg: dict, types: dict | str = "Q4_0", seed: int = 0, tied: bool 
             "w_down": w("w_down", ne, nf, 0.5 / np.sqrt(nf)),
         })
     return m
+
+
+def random_blocks(t, n_out: int, n_in: int, scale: float, rng) -> np.ndarray:
+    """Valid random GGUF rows, generated directly as bytes (fast, for full-size bench models):
+    block scales near `scale` (values of magnitude ~scale), random quants. F16/F32 fall back to
+    quantize() of normal values."""
+    tid = gb.type_id(t)
+    be, bb = gb.BLOCK[tid]
+    if be == 1:
+        return gb.quantize(t, (rng.standard_normal((n_out, n_in)) * scale).astype(np.float32))
+    nb = n_in // be
+    out = rng.integers(0, 256, size=(n_out, nb, bb), dtype=np.uint8)
+    d = (scale * (0.5 + rng.random((n_out, nb)))).astype(np.float32)
+    if tid == 2:    # Q4_0: d * (nibble - 8), |values| <= 8d
+        d /= 8
+    elif tid == 3:  # Q4_1: d * nibble + m
+        d /= 8
+        out[..., 2:4] = (-8 * d).astype(np.float16).view(np.uint8).reshape(n_out, nb, 2)
+    elif tid == 8:  # Q8_0: d * int8
+        d /= 128
+    elif tid == 14:  # Q6_K: d * scale_j * (q - 32), scales int8 in [1, 127]
+        sc = rng.integers(1, 128, size=(n_out, nb, 16), dtype=np.int8)
+        out[..., 192:208] = sc.view(np.uint8)
+        d /= 32 * 64
+    off = 208 if tid == 14 else 0
+    out[..., off:off + 2] = d.astype(np.float16).view(np.uint8).reshape(n_out, nb, 2)
+    return out.reshape(n_out, nb * bb)
+
+
+def make_bench_model(cfg: dict, t: str = "Q4_0", seed: int = 0) -> dict:
+    """A full-size model with random-byte weights of type t (tied embeddings, as Llama-3.2-3B)."""
+    rng = np.random.default_rng(seed)
+    ne, hd, nf, nv = cfg["n_embd"], cfg["head_dim"], cfg["n_ff"], cfg["n_vocab"]
+    qd, kvd = cfg["n_head"] * hd, cfg["n_head_kv"] * hd
+
+    def w(n_out, n_in, scale):
+        return (t, random_blocks(t, n_out, n_in, scale, rng))
+
+    m = {"cfg": dict(cfg), "rope_inv_freq": rope_inv_freq(cfg["rope_theta"], hd), "layers": []}
+    m["tok_embd"] = w(nv, ne, 1.0)
+    m["output"] = m["tok_embd"]
+    m["output_norm"] = np.ones(ne, np.float32)
+    for _ in range(cfg["n_layer"]):
+        m["layers"].append({
+            "attn_norm": np.ones(ne, np.float32), "ffn_norm": np.ones(ne, np.float32),
+            "wq": w(qd, ne, 1 / np.sqrt(ne)), "wk": w(kvd, ne, 1 / np.sqrt(ne)), "wv": w(kvd, ne, 1 / np.sqrt(ne)),
+            "wo": w(ne, qd, 0.5 / np.sqrt(qd)), "w_gate": w(nf, ne, 1 / np.sqrt(ne)),
+            "w_up": w(nf, ne, 1 / np.sqrt(ne)), "w_down": w(ne, nf, 0.5 / np.sqrt(nf)),
+        })
+    return m
+
+
+def weight_bytes(m: dict) -> int:
+    """Bytes of all weight tensors (the embedding table counted once when tied)."""
+    total = m["tok_embd"][1].nbytes + (0 if m["output"] is m["tok_embd"] else m["output"][1].nbytes)
+    for L in m["layers"]:
+        total += sum(v[1].nbytes for k, v in L.items() if isinstance(v, tuple))
+    return total
