@@ -1,0 +1,208 @@
+// test_hip_backend.cpp — exercises ingot::HipBackend (the C++ Llama forward above the C ABIs)
+// as Ingot's engine drives a Backend: token-by-token decode (forward), a prompt chunk
+// (forward_batch) followed by decode steps, and the reference's range errors
+// (src/metal_backend.mm:421-424). The model is a small synthetic Llama with GGUF-layout weights
+// (F16, Q8_0 and Q4_0 encoded here with ggml's published quantizers, tied Q8_0 embeddings); the
+// logits are compared with the CPU oracle's forward (oracle/model_oracle.cpp, test
+// infrastructure) over the same bytes. Tolerances (relative L2 of the logits): decode 1e-4
+// (f32 arithmetic on both sides); a chunk and the steps after it 5e-3 (the batched path rounds
+// activations and weights to f16, as the reference's Metal path does; the oracle applies the
+// same roundings). Prints one line per check and "ALL PASSED"; exits non-zero on a failure.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../../oracle/attn_oracle.h"
+#include "ingot_hip_backend.hpp"
+
+namespace {
+
+int g_fail = 0;
+
+void expect(bool ok, const std::string& what) {
+    std::printf("%s %s\n", ok ? "ok  " : "FAIL", what.c_str());
+    if (!ok) g_fail++;
+}
+
+uint16_t f16(float x) {
+    uint16_t h;
+    oracle_f32_to_f16(&x, &h, 1);
+    return h;
+}
+
+// quantize_row_q8_0 / quantize_row_q4_0 (ggml's reference quantizers), one row.
+std::vector<uint8_t> encode(uint32_t type, const float* x, int n) {
+    std::vector<uint8_t> out;
+    if (type == 1) {
+        out.resize(size_t(n) * 2);
+        for (int i = 0; i < n; i++) {
+            const uint16_t h = f16(x[i]);
+            std::memcpy(&out[2 * size_t(i)], &h, 2);
+        }
+        return out;
+    }
+    for (int b = 0; b < n / 32; b++) {
+        const float* v = x + 32 * b;
+        if (type == 8) {
+            float amax = 0;
+            for (int i = 0; i < 32; i++) amax = std::max(amax, std::fabs(v[i]));
+            const float d = amax / 127.f, id = d ? 1.f / d : 0.f;
+            const uint16_t dh = f16(d);
+            out.push_back(uint8_t(dh & 0xFF));
+            out.push_back(uint8_t(dh >> 8));
+            for (int i = 0; i < 32; i++) out.push_back(uint8_t(int8_t(roundf(v[i] * id))));
+        } else {  // Q4_0
+            float amax = 0, mx = 0;
+            for (int i = 0; i < 32; i++)
+                if (std::fabs(v[i]) > amax) { amax = std::fabs(v[i]); mx = v[i]; }
+            const float d = mx / -8.f, id = d ? 1.f / d : 0.f;
+            const uint16_t dh = f16(d);
+            out.push_back(uint8_t(dh & 0xFF));
+            out.push_back(uint8_t(dh >> 8));
+            for (int i = 0; i < 16; i++) {
+                const int a = std::min(15, int(int8_t(v[i] * id + 8.5f)));
+                const int c = std::min(15, int(int8_t(v[i + 16] * id + 8.5f)));
+                out.push_back(uint8_t(a | (c << 4)));
+            }
+        }
+    }
+    return out;
+}
+
+struct Owned {
+    std::vector<std::vector<uint8_t>> blobs;
+    ingot::HostTensor make(uint32_t type, int n_out, int n_in, float scale, std::mt19937& rng) {
+        std::normal_distribution<float> nd(0.f, scale);
+        std::vector<uint8_t> bytes;
+        std::vector<float> row(static_cast<size_t>(n_in));
+        for (int r = 0; r < n_out; r++) {
+            for (float& v : row) v = nd(rng);
+            const std::vector<uint8_t> e = encode(type, row.data(), n_in);
+            bytes.insert(bytes.end(), e.begin(), e.end());
+        }
+        blobs.push_back(std::move(bytes));
+        return ingot::HostTensor{type, uint64_t(n_in), uint64_t(n_out), blobs.back().data()};
+    }
+};
+
+double rel_l2(const float* a, const float* b, int n) {
+    double num = 0, den = 0;
+    for (int i = 0; i < n; i++) {
+        const double d = double(a[i]) - b[i];
+        num += d * d;
+        den += double(b[i]) * b[i];
+    }
+    return std::sqrt(num / den);
+}
+
+}  // namespace
+
+int main() {
+    try {
+        ingot::HostModel m;
+        m.n_layer = 2; m.n_embd = 512; m.n_head = 4; m.n_head_kv = 2; m.head_dim = 128;
+        m.n_ff = 1024; m.n_vocab = 500; m.rms_eps = 1e-5f;
+        std::mt19937 rng(11);
+        Owned own;
+        own.blobs.reserve(64);
+        std::normal_distribution<float> nd(0.f, 0.1f);
+        const int qd = m.n_head * m.head_dim, kvd = m.n_head_kv * m.head_dim;
+        m.tok_embd = own.make(8, m.n_vocab, m.n_embd, 1.f, rng);
+        m.output = m.tok_embd;  // tied
+        m.output_norm.resize(size_t(m.n_embd));
+        for (float& v : m.output_norm) v = 1.f + nd(rng);
+        m.rope_inv_freq.resize(size_t(m.head_dim / 2));
+        oracle_rope_inv_freq(500000.f, m.head_dim, nullptr, m.rope_inv_freq.data());
+        for (int l = 0; l < m.n_layer; l++) {
+            ingot::HostLayer L;
+            L.attn_norm.resize(size_t(m.n_embd));
+            L.ffn_norm.resize(size_t(m.n_embd));
+            for (float& v : L.attn_norm) v = 1.f + nd(rng);
+            for (float& v : L.ffn_norm) v = 1.f + nd(rng);
+            const float s = 1.f / std::sqrt(float(m.n_embd));
+            L.wq = own.make(2, qd, m.n_embd, s, rng);
+            L.wk = own.make(1, kvd, m.n_embd, s, rng);
+            L.wv = own.make(8, kvd, m.n_embd, s, rng);
+            L.wo = own.make(2, m.n_embd, qd, 0.5f / std::sqrt(float(qd)), rng);
+            L.w_gate = own.make(8, m.n_ff, m.n_embd, s, rng);
+            L.w_up = own.make(1, m.n_ff, m.n_embd, s, rng);
+            L.w_down = own.make(2, m.n_embd, m.n_ff, 0.5f / std::sqrt(float(m.n_ff)), rng);
+            m.layers.push_back(L);
+        }
+
+        // the oracle's view of the same bytes
+        std::vector<OracleLayer> ol;
+        for (const ingot::HostLayer& L : m.layers) {
+            auto t = [](const ingot::HostTensor& x) { return OracleTensor{int(x.type), x.data}; };
+            ol.push_back(OracleLayer{L.attn_norm.data(), L.ffn_norm.data(), t(L.wq), t(L.wk), t(L.wv), t(L.wo),
+                                     t(L.w_gate), t(L.w_up), t(L.w_down)});
+        }
+        OracleModel om{m.n_layer, m.n_embd, m.n_head, m.n_head_kv, m.head_dim, m.n_ff, m.n_vocab, m.rms_eps,
+                       m.rope_inv_freq.data(), OracleTensor{8, m.tok_embd.data}, OracleTensor{8, m.output.data},
+                       m.output_norm.data(), ol.data()};
+        const int n_ctx = 96;
+        std::vector<uint16_t> kc(size_t(m.n_layer) * n_ctx * kvd), vc(kc.size());
+        std::vector<float> want(size_t(m.n_vocab));
+        std::uniform_int_distribution<int> tok(0, m.n_vocab - 1);
+        std::vector<int32_t> toks(60);
+        for (int32_t& t : toks) t = tok(rng);
+
+        {   // token by token
+            ingot::HipBackend b(m, n_ctx, 8);
+            expect(std::string(b.name()) == "hip" && b.n_ctx() == n_ctx, "name and n_ctx");
+            for (int p = 0; p < 6; p++) {
+                const float* got = b.forward(toks[size_t(p)], p);
+                oracle_forward(&om, kc.data(), vc.data(), n_ctx, toks[size_t(p)], p, want.data(), 0, 8);
+                const double r = rel_l2(got, want.data(), m.n_vocab);
+                char buf[96];
+                std::snprintf(buf, sizeof buf, "decode pos %d: rel-L2 %.3e", p, r);
+                expect(r <= 1e-4, buf);
+            }
+        }
+        {   // a 40-token chunk, then decode steps
+            ingot::HipBackend b(m, n_ctx, 48);
+            const int n = 40;
+            const float* got = b.forward_batch(toks.data(), n, 0);
+            for (int p = 0; p < n; p++)
+                oracle_forward(&om, kc.data(), vc.data(), n_ctx, toks[size_t(p)], p, want.data(), 1, 8);
+            double r = rel_l2(got, want.data(), m.n_vocab);
+            char buf[96];
+            std::snprintf(buf, sizeof buf, "prefill 40 tokens: rel-L2 %.3e", r);
+            expect(r <= 5e-3, buf);
+            for (int p = n; p < n + 3; p++) {
+                got = b.forward(toks[size_t(p)], p);
+                oracle_forward(&om, kc.data(), vc.data(), n_ctx, toks[size_t(p)], p, want.data(), 0, 8);
+                r = rel_l2(got, want.data(), m.n_vocab);
+                std::snprintf(buf, sizeof buf, "decode after prefill pos %d: rel-L2 %.3e", p, r);
+                expect(r <= 5e-3, buf);
+            }
+            auto throws = [&](auto fn, const char* msg) {
+                try {
+                    fn();
+                } catch (const std::runtime_error& e) {
+                    return std::string(e.what()).find(msg) != std::string::npos;
+                }
+                return false;
+            };
+            expect(throws([&] { b.forward_batch(toks.data(), 49, 0); }, "batch size out of range"),
+                   "batch size error");
+            expect(throws([&] { b.forward_batch(toks.data(), 2, n_ctx - 1); }, "context window exceeded"),
+                   "context error");
+            const int32_t bad[2] = {1, m.n_vocab};
+            expect(throws([&] { b.forward_batch(bad, 2, 0); }, "token id out of range"), "token id error");
+        }
+    } catch (const std::exception& e) {
+        std::printf("FAIL exception: %s\n", e.what());
+        return 1;
+    }
+    if (g_fail) {
+        std::printf("%d FAILED\n", g_fail);
+        return 1;
+    }
+    std::printf("ALL PASSED\n");
+    return 0;
+}

@@ -14,6 +14,7 @@ pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "cpp", "test_hip_attention")
+EXE_BACKEND = os.path.join(ROOT, "tests", "cpp", "test_hip_backend")
 
 
 def test_cpp_host_side():
@@ -21,5 +22,18 @@ def test_cpp_host_side():
         subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp")], check=True)
     print("[cpp host] running tests/cpp/test_hip_attention", flush=True)
     r = subprocess.run([EXE], capture_output=True, text=True, timeout=100)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0 and "ALL PASSED" in r.stdout
+
+
+def test_cpp_backend():
+    """ingot::HipBackend (host/ingot_hip_backend.hpp): the whole Llama forward in C++ on a small
+    synthetic model with F16/Q8_0/Q4_0 weights and tied embeddings, token-by-token decode and a
+    40-token chunk then decode, against the CPU oracle forward; the checks and tolerances are in
+    tests/cpp/test_hip_backend.cpp."""
+    if not os.path.exists(EXE_BACKEND):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp")], check=True)
+    print("[cpp host] running tests/cpp/test_hip_backend", flush=True)
+    r = subprocess.run([EXE_BACKEND], capture_output=True, text=True, timeout=100)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 0 and "ALL PASSED" in r.stdout
