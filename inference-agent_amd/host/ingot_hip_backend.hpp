@@ -56,8 +56,11 @@ struct HostModel {
 
 class HipBackend {
 public:
-    HipBackend(const HostModel& m, int n_ctx, int n_batch, hipStream_t stream = nullptr)
-        : m_(m), n_ctx_(n_ctx), n_batch_(n_batch), stream_(stream) {
+    // device_weights: the matrices' `data` are device addresses already (gguf::DeviceWeights);
+    // otherwise they are host bytes and are copied to the device here.
+    HipBackend(const HostModel& m, int n_ctx, int n_batch, hipStream_t stream = nullptr,
+               bool device_weights = false)
+        : m_(m), n_ctx_(n_ctx), n_batch_(n_batch), stream_(stream), device_weights_(device_weights) {
         if (n_batch < 1) throw std::runtime_error("hip: --batch must be at least 1");
         if (int(m.layers.size()) != m.n_layer) throw std::runtime_error("hip: layer table size mismatch");
         HipAttention::Config ac;
@@ -197,6 +200,7 @@ private:
         const size_t bytes = ingot_linear_weight_bytes(&d);
         if (bytes == 0)
             throw std::runtime_error(std::string("hip: no kernel for the type of tensor ") + what);
+        if (device_weights_) return Dev{t.type, t.data, uint32_t(n_in), uint32_t(n_out)};
         void* p = alloc_bytes(bytes);
         check(hipMemcpy(p, t.data, bytes, hipMemcpyHostToDevice), what);
         return Dev{t.type, p, uint32_t(n_in), uint32_t(n_out)};
@@ -213,6 +217,7 @@ private:
     const HostModel& m_;
     int n_ctx_, n_batch_;
     hipStream_t stream_;
+    bool device_weights_;
     std::unique_ptr<HipAttention> attn_;
     size_t q_dim_ = 0, kv_dim_ = 0;
     Dev embd_, output_;

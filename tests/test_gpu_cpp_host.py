@@ -15,6 +15,7 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 EXE = os.path.join(ROOT, "tests", "cpp", "test_hip_attention")
 EXE_BACKEND = os.path.join(ROOT, "tests", "cpp", "test_hip_backend")
+EXE_GGUF = os.path.join(ROOT, "tests", "cpp", "test_gguf")
 
 
 def test_cpp_host_side():
@@ -35,5 +36,17 @@ def test_cpp_backend():
         subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp")], check=True)
     print("[cpp host] running tests/cpp/test_hip_backend", flush=True)
     r = subprocess.run([EXE_BACKEND], capture_output=True, text=True, timeout=100)
+    print(r.stdout, r.stderr, flush=True)
+    assert r.returncode == 0 and "ALL PASSED" in r.stdout
+
+
+def test_cpp_gguf():
+    """host/ingot_gguf.hpp: a GGUF file written by the test, mapped, parsed, resolved into the
+    model, its weights uploaded once, and run by HipBackend bit-identically to the in-memory
+    model; malformed files raise the reference's errors (tests/cpp/test_gguf.cpp)."""
+    if not os.path.exists(EXE_GGUF):
+        subprocess.run(["make", "-C", os.path.join(ROOT, "tests", "cpp")], check=True)
+    print("[cpp host] running tests/cpp/test_gguf", flush=True)
+    r = subprocess.run([EXE_GGUF], capture_output=True, text=True, timeout=100)
     print(r.stdout, r.stderr, flush=True)
     assert r.returncode == 0 and "ALL PASSED" in r.stdout
