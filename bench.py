@@ -56,6 +56,8 @@ LINEAR = {"wo1-f16": ("F16", 1), "wo1-q8": ("Q8_0", 1), "wo1-q4": ("Q4_0", 1), "
 # name -> weight type: the whole Llama-3.2-3B forward pass (28 layers, tied embeddings) with
 # random-byte weights, one decode token at position 128 and a 512-token prefill chunk at 0
 MODEL = {"model-q4": "Q4_0"}
+MODEL_PHASES = {"model-q4": (("decode", 1, 128), ("prefill", 512, 0)),
+                "model-q4-decode": (("decode", 1, 128),), "model-q4-prefill": (("prefill", 512, 0),)}
 # name -> (pos, n_tok): the KV-store step before attention, for a prefill chunk and a decode token
 KVSTORE = {"kv512": ("kv-store-512@3584", 3584, 512), "kv1": ("kv-store-1@4095", 4095, 1)}
 
@@ -343,11 +345,12 @@ def main():
         del b
         torch.cuda.empty_cache()
 
-    for key, t in MODEL.items():
-        if not want(key, "model"):
+    for key, phases in MODEL_PHASES.items():
+        if not (sel in ("model", key) or (sel == "all" and key == "model-q4")):
             continue
+        t = MODEL[key[:8]]
         entry = {}
-        for phase, n_tok, pos in (("decode", 1, 128), ("prefill", 512, 0)):
+        for phase, n_tok, pos in phases:
             b = ModelBench(torch, t, n_tok, pos)
             steps = max(5, args.steps // 5)
             sps = time_steps(torch, b.step, steps, args.warmup, use_graph)

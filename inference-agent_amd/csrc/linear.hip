@@ -107,6 +107,46 @@ __device__ __forceinline__ void deq8(const uint8_t* row, uint32_t k, float w[8])
     }
 }
 
+// dot(elements k..k+7 of the row, x0|x1) for the block types, without materializing each
+// weight: the group's quants are converted a byte at a time (unsigned bytes, so Q8_0's int8 are
+// biased by +128) and the block offset/scale applied once per group:
+//   Q4_0  d * (sum q x - 8 sum x)      Q4_1  d * sum q x + m * sum x
+//   Q8_0  d * (sum (q+128) x - 128 sum x)
+// The same value as the per-element form up to f32 rounding (CPU dot_q4_0 / dot_q8_0 also sum
+// the integer products per block and scale once, src/ops.cpp:153-187).
+template <int T>
+__device__ __forceinline__ float bytes_dot4(uint32_t w, const float4v& x) {
+    float s = float(w & 0xFF) * x[0];
+    s += float((w >> 8) & 0xFF) * x[1];
+    s += float((w >> 16) & 0xFF) * x[2];
+    s += float(w >> 24) * x[3];
+    return s;
+}
+
+template <int T>
+__device__ __forceinline__ float dot8(const uint8_t* row, uint32_t k, const float4v& x0, const float4v& x1) {
+    const float sx = ((x0[0] + x0[1]) + (x0[2] + x0[3])) + ((x1[0] + x1[1]) + (x1[2] + x1[3]));
+    if constexpr (T == kQ8_0) {
+        const uint8_t* b = row + 34 * (k / 32);
+        const float d = f16_bits(ld_u16(b));
+        uint32_t lo, hi;
+        ld_8bytes(b + 2 + k % 32, lo, hi);
+        const float s = bytes_dot4<T>(lo ^ 0x80808080u, x0) + bytes_dot4<T>(hi ^ 0x80808080u, x1);
+        return d * (s - 128.f * sx);
+    } else {
+        constexpr int kBytes = T == kQ4_0 ? 18 : 20, kQs = T == kQ4_0 ? 2 : 4;
+        const uint8_t* b = row + kBytes * (k / 32);
+        const uint32_t off = k % 32;
+        const float d = f16_bits(ld_u16(b));
+        uint32_t lo, hi;
+        ld_8bytes(b + kQs + (off & 15), lo, hi);
+        const uint32_t sh = off >= 16 ? 4 : 0;
+        const float s = bytes_dot4<T>((lo >> sh) & 0x0F0F0F0Fu, x0) + bytes_dot4<T>((hi >> sh) & 0x0F0F0F0Fu, x1);
+        if constexpr (T == kQ4_0) return d * (s - 8.f * sx);
+        else return d * s + f16_bits(ld_u16(b + 2)) * sx;
+    }
+}
+
 template <int T> struct Fmt;
 template <> struct Fmt<kF32>  { static constexpr uint32_t blk = 1,   bytes = 4; };
 template <> struct Fmt<kF16>  { static constexpr uint32_t blk = 1,   bytes = 2; };
@@ -125,67 +165,116 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // ---------------------------------------------------------------- one token
 
-constexpr int kMvMaxRows = 8;
-constexpr uint32_t kMvLdsRows = 32768;  // bytes of weight rows staged per workgroup (at most)
+constexpr uint32_t kMvLdsBytes = 160 * 1024;  // weight rows + x staged per workgroup (at most)
+constexpr int kMvChunks = 8;  // 16-byte staging loads per thread per round (one round up to 32 KB)
 
+// R weight rows per workgroup of 4 waves; each wave takes a quarter of the 8-element groups of
+// all R rows, reads x for a group once and applies it to the R rows (x dominates the LDS reads
+// otherwise: 32 bytes per group against ~10 for a Q4_0 row). x, and for the block-quantized types
+// the rows' bytes, are staged in LDS by one pass of 16-byte loads, all issued before the first
+// wait; rows of plain F32/F16/BF16 elements (every group a 16- or 32-byte aligned piece) are read
+// straight from memory. Rows past n_out are computed from a clamped row and not written.
 template <int T>
+constexpr bool kMvStageW = !(T == kF32 || T == kF16 || T == kBF16);
+
+template <int T, int R>
 __global__ __launch_bounds__(256) void linear_matvec_kernel(
     const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ out,
-    uint32_t n_in, uint32_t n_out, uint32_t rows_per_wg, uint32_t row_bytes, uint64_t w_bytes,
-    uint32_t accumulate) {
+    uint32_t n_in, uint32_t n_out, uint32_t row_bytes, uint64_t w_bytes, uint32_t accumulate) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const uint32_t row0 = blockIdx.x * rows_per_wg;
-    const uint32_t nrows = min(rows_per_wg, n_out - row0);
+    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t nrows = min(uint32_t(R), n_out - row0);
 
-    // Stage the rows' bytes [start, start + nrows*row_bytes) from a 16-byte aligned address.
+    // x first ([n_in] f32, 16-byte chunks), then the rows' bytes from a 16-byte aligned start.
+    const uint32_t xchunks = n_in / 4;
     const uint64_t start = uint64_t(row0) * row_bytes;
     const uint64_t a0 = start & ~uint64_t(15);
     const uint32_t shift = uint32_t(start - a0);
-    const uint32_t span = shift + nrows * row_bytes;
-    const uint32_t nchunks = (span + 15) / 16;
+    const uint32_t wchunks = kMvStageW<T> ? (shift + nrows * row_bytes + 15) / 16 : 0;
+    const uint32_t nchunks = xchunks + wchunks;
     const uint64_t left = w_bytes - a0;
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+    const __amdgpu_buffer_rsrc_t ws = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(W + a0), 0, int(left < 0x7fffffffu ? left : 0x7fffffffu), kBufferFlags);
-    for (uint32_t c = tid; c < nchunks; c += 256)
-        *reinterpret_cast<u32x4*>(smem + 16 * c) =
-            __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, int(16 * c), 0, 0));
-    float* red = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4 waves][kMvMaxRows]
-
-    // This wave's share of the 8-element groups, and x for them, loaded while the copy lands.
-    const uint32_t groups = n_in / 8, per_wave = (groups + 3) / 4;
-    const uint32_t g_begin = wave * per_wave, g_end = min(groups, g_begin + per_wave);
+    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0,
+                                                                        int(4 * n_in), kBufferFlags);
+    for (uint32_t base = 0; base < nchunks; base += 256 * kMvChunks) {
+        u32x4 st[kMvChunks];
+#pragma unroll
+        for (int i = 0; i < kMvChunks; i++) {
+            if (base + 256u * i >= nchunks) break;  // workgroup-uniform: only chunks that exist
+            const uint32_t c = min(base + tid + 256 * i, nchunks - 1);
+            st[i] = __builtin_bit_cast(u32x4, c < xchunks ? __builtin_amdgcn_raw_buffer_load_b128(xs, int(16 * c), 0, 0)
+                                                          : __builtin_amdgcn_raw_buffer_load_b128(ws, int(16 * (c - xchunks)), 0, 0));
+        }
+#pragma unroll
+        for (int i = 0; i < kMvChunks; i++) {
+            const uint32_t c = base + tid + 256 * i;
+            if (base + 256u * i >= nchunks) break;
+            if (c < nchunks) *reinterpret_cast<u32x4*>(smem + 16 * c) = st[i];
+        }
+    }
+    float* red = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4 waves][R]
     __syncthreads();
 
-    float acc[kMvMaxRows];
+    const float* xl = reinterpret_cast<const float*>(smem);
+    const uint32_t groups = n_in / 8, per_wave = (groups + 3) / 4;
+    const uint32_t g_begin = wave * per_wave, g_end = min(groups, g_begin + per_wave);
+    float acc[R];
 #pragma unroll
-    for (int r = 0; r < kMvMaxRows; r++) acc[r] = 0.f;
-    const uint8_t* rows = smem + shift;
-    for (uint32_t g = g_begin + lane; g < g_end; g += 64) {
-        const float4v x0 = *reinterpret_cast<const float4v*>(x + 8 * g);
-        const float4v x1 = *reinterpret_cast<const float4v*>(x + 8 * g + 4);
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    if constexpr (kMvStageW<T>) {
+        const uint8_t* rows = smem + 16 * xchunks + shift;
+        for (uint32_t g = g_begin + lane; g < g_end; g += 64) {
+            const float4v x0 = *reinterpret_cast<const float4v*>(xl + 8 * g);
+            const float4v x1 = *reinterpret_cast<const float4v*>(xl + 8 * g + 4);
 #pragma unroll
-        for (int r = 0; r < kMvMaxRows; r++) {
-            if (uint32_t(r) < nrows) {
+            for (int r = 0; r < R; r++) {
+                const uint8_t* row = rows + min(uint32_t(r), nrows - 1) * row_bytes;
+                if constexpr (T == kQ8_0 || T == kQ4_0 || T == kQ4_1) {
+                    acc[r] += dot8<T>(row, 8 * g, x0, x1);
+                } else {
+                    float w[8];
+                    deq8<T>(row, 8 * g, w);
+                    float s = 0.f;
+                    for (int i = 0; i < 4; i++) s += w[i] * x0[i];
+                    for (int i = 0; i < 4; i++) s += w[i + 4] * x1[i];
+                    acc[r] += s;
+                }
+            }
+        }
+    } else {
+        constexpr uint32_t GB = T == kF32 ? 32 : 16;  // bytes per 8-element group
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(W + start), 0, int(nrows * row_bytes), kBufferFlags);
+        for (uint32_t g = g_begin + lane; g < g_end; g += 64) {
+            u32x4 raw[R][GB / 16];
+#pragma unroll
+            for (int r = 0; r < R; r++)
+                for (uint32_t q = 0; q < GB / 16; q++)
+                    raw[r][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                             rs, int(min(uint32_t(r), nrows - 1) * row_bytes + g * GB + 16 * q), 0, 0));
+            const float4v x0 = *reinterpret_cast<const float4v*>(xl + 8 * g);
+            const float4v x1 = *reinterpret_cast<const float4v*>(xl + 8 * g + 4);
+#pragma unroll
+            for (int r = 0; r < R; r++) {
                 float w[8];
-                deq8<T>(rows + r * row_bytes, 8 * g, w);
-                float s = acc[r];
+                deq8<T>(reinterpret_cast<const uint8_t*>(&raw[r][0]), 0, w);
+                float s = 0.f;
                 for (int i = 0; i < 4; i++) s += w[i] * x0[i];
                 for (int i = 0; i < 4; i++) s += w[i + 4] * x1[i];
-                acc[r] = s;
+                acc[r] += s;
             }
         }
     }
 #pragma unroll
-    for (int r = 0; r < kMvMaxRows; r++) {
-        if (uint32_t(r) < nrows) {
-            const float s = wave_sum(acc[r]);
-            if (lane == 0) red[wave * kMvMaxRows + r] = s;
-        }
+    for (int r = 0; r < R; r++) {
+        const float s = wave_sum(acc[r]);
+        if (lane == 0) red[wave * R + r] = s;
     }
     __syncthreads();
     if (tid < nrows) {
-        const float s = (red[tid] + red[kMvMaxRows + tid]) + (red[2 * kMvMaxRows + tid] + red[3 * kMvMaxRows + tid]);
+        const float s = (red[tid] + red[R + tid]) + (red[2 * R + tid] + red[3 * R + tid]);
         float* o = out + row0 + tid;
         *o = accumulate ? *o + s : s;
     }
@@ -560,15 +649,29 @@ int launch_t(const uint8_t* W, const float* x, float* out, uint32_t n_in, uint32
              size_t workspace_bytes, hipStream_t stream) {
     const uint32_t row_bytes = n_in / Fmt<T>::blk * Fmt<T>::bytes;
     if (n_tok == 1) {
-        uint32_t r = kMvLdsRows / row_bytes;
-        r = r < 1 ? 1 : r > kMvMaxRows ? kMvMaxRows : r;
-        // Keep at least ~3 workgroups per CU on the 256-CU part.
-        const uint32_t fill = (n_out + 767) / 768;
-        if (r > fill) r = fill < 1 ? 1 : fill;
-        const uint32_t blocks = (n_out + r - 1) / r;
-        const size_t lds = ((size_t(r) * row_bytes + 15 + 15) / 16) * 16 + 4 * kMvMaxRows * sizeof(float);
-        hipLaunchKernelGGL(linear_matvec_kernel<T>, dim3(blocks), dim3(256), lds, stream, W, x, out,
-                           n_in, n_out, r, row_bytes, uint64_t(n_out) * row_bytes, accumulate);
+        // Eight rows per workgroup when they (and x) fit the staging buffer and the grid still
+        // has >= 3 workgroups per CU; four rows otherwise.
+        const size_t xb = size_t(n_in) * 4;
+        const size_t wrow = kMvStageW<T> ? row_bytes : 0;  // staged bytes per row
+        // Eight rows per workgroup when that still leaves >= 3 workgroups per CU (measured:
+        // fewer, larger workgroups are slower here, more rows per workgroup only pay for x
+        // traffic, which is not the limit), four otherwise.
+        uint32_t R = 4;
+        if (n_out / 8 >= 768 && xb + 8 * wrow + 16 + 4 * 8 * 4 <= kMvLdsBytes) R = 8;
+        if (xb + size_t(R) * wrow + 16 + 4 * R * 4 > kMvLdsBytes) return -2;  // rows too long to stage
+        const uint32_t blocks = (n_out + R - 1) / R;
+        const size_t lds = (xb + size_t(R) * wrow + 16 + 15) / 16 * 16 + 4 * R * sizeof(float);
+        auto launch = [&](auto kernel) {
+            static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                               int(kMvLdsBytes));
+            if (attr != hipSuccess) return -4;
+            hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, stream, W, x, out, n_in, n_out, row_bytes,
+                               uint64_t(n_out) * row_bytes, accumulate);
+            return 0;
+        };
+        const int rc = R == 8 ? launch(linear_matvec_kernel<T, 8>) : launch(linear_matvec_kernel<T, 4>);
+        if (rc) return rc;
     } else {
         const uint32_t tiles_n = (n_out + kMmRows - 1) / kMmRows;
         const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
