@@ -73,22 +73,37 @@ __global__ __launch_bounds__(64 * QW * KG) __attribute__((amdgpu_waves_per_eu(G 
 void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict__ K,
                          const _Float16* __restrict__ V, float* __restrict__ out,
                          float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
-                         uint32_t n_head_kv, uint32_t n_splits, float qscale) {
+                         uint32_t n_head_kv, uint32_t tps, float qscale) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
     const int qw = wave % QW, kg = wave / QW;  // query sub-block, key group
     const int li = lane & 15, g = lane >> 4;
-    const uint32_t kvh = blockIdx.y, split = blockIdx.z;
+    // 1-D grid: workgroup b serves KV head b % n_head_kv, so with 8 KV heads each XCD (b % 8)
+    // holds one head's K/V and Q in its L2 for all of that head's query blocks and splits.
+    // b / n_head_kv enumerates (query block, key split) pairs, the longest query blocks first:
+    // block j sees ntiles_j key tiles and is split into n_splits_j = ceil(ntiles_j / tps)
+    // near-equal key ranges, so no workgroup walks more than tps tiles (the causal chunk's last
+    // block no longer sets the critical path alone).
+    const uint32_t kvh = blockIdx.x % n_head_kv;
     const size_t kv_dim = size_t(n_head_kv) * kHeadDim;
-    const uint32_t qblk0 = blockIdx.x * 16 * QW;
+    uint32_t qblk = (n_tok + 16 * QW - 1) / (16 * QW), split = blockIdx.x / n_head_kv, n_splits = 1;
+    uint32_t ntiles = 0;
+    while (qblk > 0) {
+        qblk--;
+        ntiles = (pos + min(n_tok, (qblk + 1) * 16 * QW) + kBN - 1) / kBN;
+        n_splits = (ntiles + tps - 1) / tps;
+        if (split < n_splits) break;
+        split -= n_splits;
+    }
+    if (split >= n_splits) return;  // past the enumerated pairs (the host never launches these)
+    const uint32_t qblk0 = qblk * 16 * QW;
     const uint32_t q0 = qblk0 + 16 * qw;
 
     // Keys [0, kend) are visible to some query of this workgroup.
     const uint32_t qlast_wg = min(n_tok, qblk0 + 16 * QW) - 1;
     const uint32_t kend = pos + qlast_wg + 1;
-    const uint32_t ntiles = (kend + kBN - 1) / kBN;
     const uint32_t t_begin = uint32_t((uint64_t(split) * ntiles) / n_splits);
     const uint32_t t_end = uint32_t((uint64_t(split + 1) * ntiles) / n_splits);
     // Keys [0, kend_w) are visible to some query of this wave; 0 if the wave has no queries.
@@ -135,37 +150,47 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         }
     };
 
-    // The first tile's copy goes out before anything else, so its latency overlaps the Q load.
-    uint32_t t_first = t_begin + kg;
-    if (t_begin < t_end && t_first < t_end)
-#pragma unroll
-        for (int p = 0; p < 4; p++) issue_part(t_first, 0, p);
-
     // Q is loaded once per workgroup: every thread converts part of the workgroup's
     // QW*16 queries x G heads (times scale*log2(e), to f16) into the second stage of each key
     // group, which the first tile's copy does not touch: queries 0..31 in key group 0's, 32..63
     // in key group 1's, as rows [query][head][128 dims] with the 16-byte chunk c of a row stored
     // at c ^ (query & 15), so that the B-operand reads below are bank-conflict free.
+    // All of the thread's Q loads are issued first, then the first tile's copy: loads complete
+    // in order, so the conversion waits only for Q, and the tile streams in meanwhile.
     static_assert(QW * 16 == 64 && G * 32 * 256 <= kStageBytes, "Q staging fits the free stages");
+    constexpr int kF4 = QW * 16 * G * 32;  // float4 chunks of the workgroup's Q
+    constexpr int NT = 64 * QW * KG;
+    constexpr int kQIt = (kF4 + NT - 1) / NT;
+    float4v qx[kQIt];
     {
-        constexpr int kF4 = QW * 16 * G * 32;  // float4 chunks of the workgroup's Q
-        constexpr int NT = 64 * QW * KG;
+        const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(q + size_t(qblk0) * q_stride + size_t(kvh) * G * kHeadDim), 0,
+            0x7fffffff, kBufferFlags);
 #pragma unroll
-        for (int it = 0; it < (kF4 + NT - 1) / NT; it++) {
-            const int idx = tid + it * NT;
-            if (kF4 % NT != 0 && idx >= kF4) break;
+        for (int it = 0; it < kQIt; it++) {
+            const int idx = min(tid + it * NT, kF4 - 1);
             const int ql = idx / (G * 32), rem = idx % (G * 32);
-            const int h = rem >> 5, c4 = rem & 31;
-            const uint32_t row = min(qblk0 + ql, n_tok - 1);
-            const float4v x = *reinterpret_cast<const float4v*>(
-                q + size_t(row) * q_stride + (size_t(kvh) * G + h) * kHeadDim + 4 * c4);
-            half4 y;
-#pragma unroll
-            for (int e = 0; e < 4; e++) y[e] = _Float16(x[e] * qscale);
-            char* qs = smem + ((ql >> 5) * 2 + 1) * kStageBytes;
-            const int chunk = (c4 >> 1) ^ (ql & 15);
-            *reinterpret_cast<half4*>(qs + ((ql & 31) * G + h) * kRowBytes + 16 * chunk + 8 * (c4 & 1)) = y;
+            const uint32_t row = min(qblk0 + ql, n_tok - 1) - qblk0;
+            qx[it] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                qr, int(4 * (row * q_stride + (rem >> 5) * kHeadDim + 4 * (rem & 31))), 0, 0));
         }
+    }
+    uint32_t t_first = t_begin + kg;
+    if (t_begin < t_end && t_first < t_end)
+#pragma unroll
+        for (int p = 0; p < 4; p++) issue_part(t_first, 0, p);
+#pragma unroll
+    for (int it = 0; it < kQIt; it++) {
+        const int idx = tid + it * NT;
+        if (kF4 % NT != 0 && idx >= kF4) break;
+        const int ql = idx / (G * 32), rem = idx % (G * 32);
+        const int h = rem >> 5, c4 = rem & 31;
+        half4 y;
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = _Float16(qx[it][e] * qscale);
+        char* qs = smem + ((ql >> 5) * 2 + 1) * kStageBytes;
+        const int chunk = (c4 >> 1) ^ (ql & 15);
+        *reinterpret_cast<half4*>(qs + ((ql & 31) * G + h) * kRowBytes + 16 * chunk + 8 * (c4 & 1)) = y;
     }
     __syncthreads();
     // B operand Q^T per head: lane holds Q[q0 + li][32*ks + 8*g + e] * scale*log2(e), as f16.
@@ -370,38 +395,43 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     }
 
     if (KG == 2) {
-        // Merge the two key groups through LDS (the tiles are no longer read), one head at a
-        // time: group 1 stores its (O, m, l, started) per lane, group 0 folds it in with the
-        // log-sum-exp rule. 35 words x 64 lanes x QW waves per round.
-        constexpr int kFields = 32 + 3;
-        float* st = reinterpret_cast<float*>(smem) + qw * kFields * 64 + lane;
+        // Merge the two key groups through LDS (the tiles are no longer read): group 1 stores
+        // its (O, m, l, started) per lane for as many heads as fit (all 3 for G = 3), one
+        // barrier, group 0 folds them in with the log-sum-exp rule. 9 16-byte fields x 64 lanes
+        // x QW waves per head, lane-minor (conflict-free 16-byte LDS accesses).
+        constexpr int kFields = 9;
+        constexpr int kHR = (KG * 2 * kStageBytes) / (QW * kFields * 64 * 16);  // heads per round
+        static_assert(kHR >= 1, "merge buffer fits");
 #pragma unroll
-        for (int h = 0; h < G; h++) {
+        for (int h0 = 0; h0 < G; h0 += kHR) {
+            if (h0 > 0) __syncthreads();  // the previous round's reads are done
             if (kg == 1) {
 #pragma unroll
-                for (int d = 0; d < 8; d++)
+                for (int h = h0; h < min(G, h0 + kHR); h++) {
+                    float4v* st = reinterpret_cast<float4v*>(smem) + ((h - h0) * QW + qw) * kFields * 64 + lane;
 #pragma unroll
-                    for (int j = 0; j < 4; j++) st[(d * 4 + j) * 64] = O[h][d][j];
-                st[32 * 64] = m[h];
-                st[33 * 64] = l[h];
-                st[34 * 64] = started[h] ? 1.f : 0.f;
+                    for (int d = 0; d < 8; d++) st[d * 64] = O[h][d];
+                    st[8 * 64] = float4v{m[h], l[h], started[h] ? 1.f : 0.f, 0.f};
+                }
             }
             __syncthreads();
             if (kg == 0) {
-                const float m1 = st[32 * 64], l1 = st[33 * 64];
-                const bool s1 = st[34 * 64] != 0.f;
-                const float M = started[h] ? (s1 ? fmaxf(m[h], m1) : m[h]) : m1;
-                const float a0 = started[h] ? fast_exp2(m[h] - M) : 0.f;
-                const float a1 = s1 ? fast_exp2(m1 - M) : 0.f;
 #pragma unroll
-                for (int d = 0; d < 8; d++)
+                for (int h = h0; h < min(G, h0 + kHR); h++) {
+                    const float4v* st = reinterpret_cast<const float4v*>(smem) + ((h - h0) * QW + qw) * kFields * 64 + lane;
+                    const float4v ml = st[8 * 64];
+                    const float m1 = ml[0], l1 = ml[1];
+                    const bool s1 = ml[2] != 0.f;
+                    const float M = started[h] ? (s1 ? fmaxf(m[h], m1) : m[h]) : m1;
+                    const float a0 = started[h] ? fast_exp2(m[h] - M) : 0.f;
+                    const float a1 = s1 ? fast_exp2(m1 - M) : 0.f;
 #pragma unroll
-                    for (int j = 0; j < 4; j++) O[h][d][j] = O[h][d][j] * a0 + st[(d * 4 + j) * 64] * a1;
-                l[h] = l[h] * a0 + l1 * a1;
-                m[h] = (started[h] || s1) ? M : m[h];
-                started[h] = started[h] || s1;
+                    for (int d = 0; d < 8; d++) O[h][d] = O[h][d] * a0 + st[d * 64] * a1;
+                    l[h] = l[h] * a0 + l1 * a1;
+                    m[h] = (started[h] || s1) ? M : m[h];
+                    started[h] = started[h] || s1;
+                }
             }
-            __syncthreads();
         }
         if (kg == 1) return;
     }
@@ -439,12 +469,18 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
 // at once and folded in online (clamped indices keep them unconditional, masked entries get
 // weight 0).
 constexpr int kCombineThreads = 256;
+constexpr uint32_t kQBlock = 64;  // queries per prefill workgroup (16 x kQW)
 __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
-    const float* __restrict__ part, float* __restrict__ out, uint32_t n_tok, uint32_t n_head,
-    uint32_t q_stride, uint32_t n_splits) {
+    const float* __restrict__ part, float* __restrict__ out, uint32_t pos, uint32_t n_tok,
+    uint32_t n_head, uint32_t q_stride, uint32_t tps) {
     const uint32_t rec = blockIdx.x * (kCombineThreads / 32) + threadIdx.x / 32;
     if (rec >= n_tok * n_head) return;
     const uint32_t row = rec / n_head, h = rec % n_head;
+    // The split count of this token's query block, as the prefill kernel enumerates it; blocks
+    // of one split wrote their output directly.
+    const uint32_t blk_end = min(n_tok, (row / kQBlock + 1) * kQBlock);
+    const uint32_t n_splits = ((pos + blk_end + kBN - 1) / kBN + tps - 1) / tps;
+    if (n_splits == 1) return;
     const int d = 4 * (threadIdx.x % 32);
     const size_t sstride = size_t(n_tok) * n_head * kPartStride;
     const float* src = part + size_t(rec) * kPartStride;
@@ -480,21 +516,30 @@ template <int G>
 int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                      uint32_t n_splits, float qscale, hipStream_t stream) {
-    const dim3 grid((n_tok + 16 * kQW - 1) / (16 * kQW), n_head_kv, n_splits);
+    static_assert(16 * kQW == kQBlock, "query block size");
+    const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
+    const uint32_t tps = (max_tiles + n_splits - 1) / n_splits;  // tiles per split at most
+    uint32_t pairs = 0;  // (query block, split) pairs: the kernel's enumeration
+    for (uint32_t b = 0; b * kQBlock < n_tok; b++) {
+        const uint32_t nt = (pos + min(n_tok, (b + 1) * kQBlock) + kBN - 1) / kBN;
+        pairs += (nt + tps - 1) / tps;
+    }
+    if (uint64_t(pairs) * n_head_kv > 0x7fffffffu) return -1;
+    const dim3 grid(pairs * n_head_kv);
     const size_t lds = size_t(kKG) * 2 * kStageBytes;  // 128 KB: two double-buffered stages
     static const hipError_t attr = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&attn_prefill_kernel<G, kQW, kKG>),
         hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (attr != hipSuccess) return -4;
     hipLaunchKernelGGL((attn_prefill_kernel<G, kQW, kKG>), grid, dim3(64 * kQW * kKG), lds, stream,
-                       q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale);
+                       q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, tps, qscale);
     if (hipGetLastError() != hipSuccess) return -4;
     if (n_splits > 1) {
         const uint32_t n_head = n_head_kv * G;
         const uint32_t per_block = kCombineThreads / 32;
         hipLaunchKernelGGL(attn_prefill_combine, dim3((n_tok * n_head + per_block - 1) / per_block),
                            dim3(kCombineThreads), 0, stream, part,
-                           out, n_tok, n_head, q_stride, n_splits);
+                           out, pos, n_tok, n_head, q_stride, tps);
         if (hipGetLastError() != hipSuccess) return -4;
     }
     return 0;
@@ -504,16 +549,33 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
 
 uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t requested) {
     const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
-    uint32_t splits = requested;
-    if (splits == 0) {
-        // One 8-wave workgroup per CU (2 waves/SIMD) needs >= 256 workgroups on 256 CUs; split
-        // the key range when the query blocks alone give fewer, up to 4 ways (measured: more
-        // splits cost more in partial traffic than they gain), keeping >= 8 tiles per split.
-        const uint32_t wgs = ((n_tok + 16 * kQW - 1) / (16 * kQW)) * n_head_kv;
-        splits = (256 + wgs - 1) / wgs;
-        splits = min(min(splits, 4u), max(1u, max_tiles / 8));
+    const uint32_t cap = min(max_tiles, kMaxPrefillSplits);
+    // (query block, split) workgroups for at most s splits per block (the kernel's enumeration)
+    auto workgroups = [&](uint32_t s) {
+        const uint32_t tps = (max_tiles + s - 1) / s;
+        uint64_t pairs = 0;
+        for (uint32_t b = 0; b * kQBlock < n_tok; b++)
+            pairs += ((pos + min(n_tok, (b + 1) * kQBlock) + kBN - 1) / kBN + tps - 1) / tps;
+        return pairs * n_head_kv;
+    };
+    uint32_t s = min(requested, cap);
+    if (requested == 0) {
+        // The shortest per-workgroup key walk whose workgroups still fit one round of 8-wave
+        // workgroups on the 256 CUs (one per CU: 128 KB of LDS each), with >= 8 tiles per
+        // split: each split adds a record write (~3 us at C4's 26 MB) and the combine launch,
+        // which shorter walks do not pay back (measured: C2 20.0 us unsplit, 22.0 us with 4
+        // splits of <= 2 tiles).
+        constexpr uint32_t kMinSplitTiles = 8;
+        s = 1;
+        for (uint32_t c = 2; c <= cap; c++) {
+            if ((max_tiles + c - 1) / c < kMinSplitTiles) break;
+            if (workgroups(c) <= 256) s = c;
+        }
     }
-    return max(1u, min(splits, min(max_tiles, kMaxPrefillSplits)));
+    s = max(1u, s);
+    // The largest per-block split count that this many tiles per split gives.
+    const uint32_t tps = (max_tiles + s - 1) / s;
+    return (max_tiles + tps - 1) / tps;
 }
 
 int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
