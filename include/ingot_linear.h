@@ -74,6 +74,52 @@ size_t ingot_linear_workspace_size(const IngotLinearDesc* d);
 int ingot_linear(const void* w, const float* x, float* out, void* workspace, size_t workspace_bytes,
                  const IngotLinearDesc* d, void* stream);
 
+/* One decode token through up to three projections that read the same input, in one launch,
+ * with the per-layer step before and after fused in (ingot_proj):
+ *   prologue INGOT_PROJ_X        x' = x
+ *            INGOT_PROJ_RMSNORM  x' = x * (1 / sqrt(mean(x^2) + eps)) * norm_w — the rmsnorm
+ *                                before q/k/v and before gate/up (src/metal_backend.mm:
+ *                                433-437, 448-449; ops::rmsnorm, src/ops.cpp:226-231)
+ *   epilogue INGOT_PROJ_STORE      out[m] = W[m]·x'
+ *            INGOT_PROJ_ACCUMULATE out[m] += W[m]·x' (the residual adds after wo and w_down)
+ *            INGOT_PROJ_SILU_GATE  n_mats == 2 (gate, up), equal n_out:
+ *                                  out[0] = silu(W[0]·x') * (W[1]·x'), silu(g) = g/(1+exp(-g))
+ *                                  (encode_silu_mul, src/metal_backend.mm:411-417;
+ *                                  src/cpu_backend.cpp:77, ops::silu src/ops.h:35)
+ * The reference encodes these as separate dispatches (encode_rmsnorm, three or two
+ * encode_linear calls, encode_silu_mul: src/metal_backend.mm:433-452); the results equal those
+ * of ingot_rmsnorm, ingot_linear (n_tok == 1) and ingot_silu_mul run in sequence, bit for bit.
+ * Every matrix has the same type and n_in. */
+enum {
+    INGOT_PROJ_X = 0,
+    INGOT_PROJ_RMSNORM = 1
+};
+enum {
+    INGOT_PROJ_STORE = 0,
+    INGOT_PROJ_ACCUMULATE = 1,
+    INGOT_PROJ_SILU_GATE = 2
+};
+
+typedef struct IngotProjDesc {
+    uint32_t type;       /* GGUF tensor type id, shared by the matrices */
+    uint32_t n_in;       /* as IngotLinearDesc.n_in */
+    uint32_t n_mats;     /* 1..3 */
+    uint32_t n_out[3];   /* rows of each matrix (entries past n_mats ignored) */
+    uint32_t prologue;   /* INGOT_PROJ_X or INGOT_PROJ_RMSNORM */
+    uint32_t epilogue;   /* INGOT_PROJ_STORE, INGOT_PROJ_ACCUMULATE or INGOT_PROJ_SILU_GATE */
+    float eps;           /* rmsnorm epsilon (prologue INGOT_PROJ_RMSNORM) */
+} IngotProjDesc;
+
+/*   w       host array of n_mats device pointers to the weight bytes, each 16-byte aligned
+ *   x       [n_in] f32, 16-byte aligned
+ *   norm_w  [n_in] f32 rmsnorm weights, 16-byte aligned (INGOT_PROJ_RMSNORM; else ignored)
+ *   out     host array of n_mats device pointers, f32 [n_out[m]], 4-byte aligned, not
+ *           overlapping x or w (one pointer for INGOT_PROJ_SILU_GATE)
+ * Returns INGOT_ATTN_EUNSUPPORTED for a type without a kernel or rows too long to stage
+ * (n_in * 8 + 8 rows' bytes beyond 160 KB). */
+int ingot_proj(const void* const* w, const float* x, const float* norm_w, float* const* out,
+               const IngotProjDesc* d, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

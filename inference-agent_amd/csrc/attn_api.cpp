@@ -115,6 +115,31 @@ int ingot_linear(const void* w, const float* x, float* out, void* workspace, siz
          : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
 
+int ingot_proj(const void* const* w, const float* x, const float* norm_w, float* const* out,
+               const IngotProjDesc* d, void* stream) {
+    if (!d || !w || !x || !out || d->n_in == 0 || d->n_mats < 1 || d->n_mats > 3) return INGOT_ATTN_EINVAL;
+    if (d->prologue > INGOT_PROJ_RMSNORM || d->epilogue > INGOT_PROJ_SILU_GATE) return INGOT_ATTN_EINVAL;
+    uint32_t elems, bytes;
+    linear_block(d->type, elems, bytes);
+    if (elems == 0) return INGOT_ATTN_EUNSUPPORTED;
+    if (d->n_in % 32 != 0 || d->n_in % elems != 0) return INGOT_ATTN_EUNSUPPORTED;
+    if (!aligned16(x)) return INGOT_ATTN_EINVAL;
+    if (d->prologue == INGOT_PROJ_RMSNORM && (!norm_w || !aligned16(norm_w) || !(d->eps >= 0.f)))
+        return INGOT_ATTN_EINVAL;
+    const uint32_t n_outs = d->epilogue == INGOT_PROJ_SILU_GATE ? 1 : d->n_mats;
+    if (d->epilogue == INGOT_PROJ_SILU_GATE && (d->n_mats != 2 || d->n_out[0] != d->n_out[1]))
+        return INGOT_ATTN_EINVAL;
+    for (uint32_t m = 0; m < d->n_mats; m++)
+        if (!w[m] || !aligned16(w[m]) || d->n_out[m] == 0) return INGOT_ATTN_EINVAL;
+    if (uint64_t(d->n_in) / elems * bytes > 0x7fffffffull) return INGOT_ATTN_EUNSUPPORTED;
+    for (uint32_t m = 0; m < n_outs; m++)
+        if (!out[m] || (reinterpret_cast<uintptr_t>(out[m]) & 3u) != 0) return INGOT_ATTN_EINVAL;
+    const int lrc = ingot::launch_proj(d->type, w, x, norm_w, out, d->n_in, d->n_out, d->n_mats,
+                                       int(d->prologue), int(d->epilogue), d->eps,
+                                       static_cast<hipStream_t>(stream));
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+}
+
 uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
     if (check_decode(d)) return 0;
     return ingot::decode_splits(d->n_keys, d->n_head_kv, d->n_splits);

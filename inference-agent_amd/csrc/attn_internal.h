@@ -45,6 +45,12 @@ constexpr uint32_t kLinearMaxTiles = 256;
 int launch_linear(uint32_t type, const void* W, const float* x, float* out, uint32_t n_in,
                   uint32_t n_out, uint32_t n_tok, uint32_t accumulate, uint32_t n_splits,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+// One token through n_mats (1..3) matrices of one type sharing x, with the rmsnorm prologue
+// (pro 1, norm weights aux) and the store / accumulate / silu-gate epilogue (epi 0 / 1 / 2).
+// Returns 0, -2 (type without a kernel, rows too long to stage) or -4 (launch failed).
+int launch_proj(uint32_t type, const void* const* W, const float* x, const float* aux,
+                float* const* out, uint32_t n_in, const uint32_t* n_out, uint32_t n_mats,
+                int pro, int epi, float eps, hipStream_t stream);
 // Split count for the batched path (requested: 0 = choose); `workspace_bytes` bounds it.
 uint32_t linear_splits(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested,
                        size_t workspace_bytes);

@@ -21,6 +21,8 @@
 // one weight row — exactly one dequantization group — so each wave dequantizes its own 64 rows
 // straight from global memory into registers (prefetched one 32-wide k step ahead) and only x,
 // shared by the four waves, goes through LDS.
+#include <type_traits>
+
 #include "attn_common.h"
 #include "attn_internal.h"
 
@@ -168,44 +170,95 @@ __device__ __forceinline__ float wave_sum(float x) {
 constexpr uint32_t kMvLdsBytes = 160 * 1024;  // weight rows + x staged per workgroup (at most)
 constexpr int kMvChunks = 8;  // 16-byte staging loads per thread per round (one round up to 32 KB)
 
-// R weight rows per workgroup of 4 waves; each wave takes a quarter of the 8-element groups of
-// all R rows, reads x for a group once and applies it to the R rows (x dominates the LDS reads
-// otherwise: 32 bytes per group against ~10 for a Q4_0 row). x, and for the block-quantized types
-// the rows' bytes, are staged in LDS by one pass of 16-byte loads, all issued before the first
-// wait; rows of plain F32/F16/BF16 elements (every group a 16- or 32-byte aligned piece) are read
-// straight from memory. Rows past n_out are computed from a clamped row and not written.
+// What happens to x before the products, and to the row sums after (ingot_proj):
+//   prologue kProNone: x as given; kProRmsNorm: x * (1/sqrt(mean(x^2) + eps)) * aux, the
+//     rmsnorm that precedes q/k/v and gate/up (the same arithmetic, in the same order, as
+//     rmsnorm_kernel, so the fused and the separate sequence give identical results);
+//   epilogue kEpiStore / kEpiAccumulate: out = s or out += s per matrix; kEpiSiluGate: two
+//     matrices (gate, up) over the same rows, out0 = silu(s_gate) * s_up with
+//     silu(g) = g / (1 + exp(-g)), as silu_mul_kernel.
+enum : int { kProNone = 0, kProRmsNorm = 1 };
+enum : int { kEpiStore = 0, kEpiAccumulate = 1, kEpiSiluGate = 2 };
+
+// Up to three matrices of one type sharing n_in and x (q/k/v, gate/up), launched as one grid:
+// blocks [blk_end[m-1], blk_end[m]) take matrix m's rows, R per block.
+struct MvArgs {
+    const uint8_t* W[3];
+    float* out[3];
+    uint32_t n_out[3];
+    uint32_t blk_end[3];
+    const float* x;
+    const float* aux;  // rmsnorm weights [n_in]
+    uint32_t n_in, row_bytes;
+    float eps;
+};
+
+// R weight rows per matrix per workgroup of 4 waves (2R for the gate/up pair); each wave takes a
+// quarter of the 8-element groups of all rows, reads x for a group once and applies it to every
+// row (x dominates the LDS reads otherwise: 32 bytes per group against ~10 for a Q4_0 row). x
+// (and the rmsnorm weights), and for the block-quantized types the rows' bytes, are staged in
+// LDS by one pass of 16-byte loads, all issued before the first wait; rows of plain
+// F32/F16/BF16 elements (every group a 16- or 32-byte aligned piece) are read straight from
+// memory. Rows past n_out are computed from a clamped row and not written.
 template <int T>
 constexpr bool kMvStageW = !(T == kF32 || T == kF16 || T == kBF16);
 
-template <int T, int R>
-__global__ __launch_bounds__(256) void linear_matvec_kernel(
-    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ out,
-    uint32_t n_in, uint32_t n_out, uint32_t row_bytes, uint64_t w_bytes, uint32_t accumulate) {
+template <int T, int R, int PRO, int EPI>
+__global__ __launch_bounds__(256) void linear_matvec_kernel(const MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int NS = EPI == kEpiSiluGate ? 2 : 1;  // row sets: (gate, up) or one matrix
+    constexpr int NR = NS * R;
     const uint32_t tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
-    const uint32_t row0 = blockIdx.x * R;
+    uint32_t m = 0, blk = blockIdx.x;
+    if constexpr (EPI != kEpiSiluGate) {
+        if (blk >= a.blk_end[0]) m = blk >= a.blk_end[1] ? 2 : 1;
+        if (m > 0) blk -= a.blk_end[m - 1];
+    }
+    const uint32_t n_in = a.n_in, row_bytes = a.row_bytes;
+    const uint32_t n_out = a.n_out[m];
+    const uint32_t row0 = blk * R;
     const uint32_t nrows = min(uint32_t(R), n_out - row0);
 
-    // x first ([n_in] f32, 16-byte chunks), then the rows' bytes from a 16-byte aligned start.
+    // LDS: x ([n_in] f32, 16-byte chunks), the rmsnorm weights, then each set's rows' bytes
+    // from a 16-byte aligned start.
     const uint32_t xchunks = n_in / 4;
+    const uint32_t achunks = PRO == kProRmsNorm ? xchunks : 0;
     const uint64_t start = uint64_t(row0) * row_bytes;
     const uint64_t a0 = start & ~uint64_t(15);
     const uint32_t shift = uint32_t(start - a0);
     const uint32_t wchunks = kMvStageW<T> ? (shift + nrows * row_bytes + 15) / 16 : 0;
-    const uint32_t nchunks = xchunks + wchunks;
-    const uint64_t left = w_bytes - a0;
-    const __amdgpu_buffer_rsrc_t ws = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(W + a0), 0, int(left < 0x7fffffffu ? left : 0x7fffffffu), kBufferFlags);
-    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(x), 0,
+    const uint32_t nchunks = xchunks + achunks + NS * wchunks;
+    const uint64_t w_bytes = uint64_t(n_out) * row_bytes;
+    // Bytes from a0 to the end of the matrix, rounded up to whole dwords: buffer loads drop
+    // every dword that reaches past num_records, and a row may end mid-dword (an odd number of
+    // 18-, 34- or 210-byte rows); the dword holding the last byte never crosses a page.
+    const uint64_t left = (w_bytes - a0 + 3) & ~uint64_t(3);
+    const int wrec = int(left < 0x7fffffffu ? left : 0x7fffffffu);
+    __amdgpu_buffer_rsrc_t ws[NS];
+#pragma unroll
+    for (int s = 0; s < NS; s++)
+        ws[s] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.W[m + s] + a0), 0, wrec, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0,
                                                                         int(4 * n_in), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t as = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(PRO == kProRmsNorm ? a.aux : a.x), 0, int(4 * n_in), kBufferFlags);
     for (uint32_t base = 0; base < nchunks; base += 256 * kMvChunks) {
         u32x4 st[kMvChunks];
 #pragma unroll
         for (int i = 0; i < kMvChunks; i++) {
             if (base + 256u * i >= nchunks) break;  // workgroup-uniform: only chunks that exist
             const uint32_t c = min(base + tid + 256 * i, nchunks - 1);
-            st[i] = __builtin_bit_cast(u32x4, c < xchunks ? __builtin_amdgcn_raw_buffer_load_b128(xs, int(16 * c), 0, 0)
-                                                          : __builtin_amdgcn_raw_buffer_load_b128(ws, int(16 * (c - xchunks)), 0, 0));
+            if (c < xchunks) {
+                st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xs, int(16 * c), 0, 0));
+            } else if (PRO == kProRmsNorm && c < xchunks + achunks) {
+                st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(as, int(16 * (c - xchunks)), 0, 0));
+            } else {
+                const uint32_t cw = c - xchunks - achunks;
+                if (NS == 2 && cw >= wchunks)
+                    st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ws[NS - 1], int(16 * (cw - wchunks)), 0, 0));
+                else
+                    st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ws[0], int(16 * cw), 0, 0));
+            }
         }
 #pragma unroll
         for (int i = 0; i < kMvChunks; i++) {
@@ -214,23 +267,48 @@ __global__ __launch_bounds__(256) void linear_matvec_kernel(
             if (c < nchunks) *reinterpret_cast<u32x4*>(smem + 16 * c) = st[i];
         }
     }
-    float* red = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4 waves][R]
+    float* red = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4 waves][NR]
     __syncthreads();
 
-    const float* xl = reinterpret_cast<const float*>(smem);
+    float* xl = reinterpret_cast<float*>(smem);
+    if constexpr (PRO == kProRmsNorm) {
+        // rmsnorm_kernel's reduction: float4 per thread strided by 1024 elements, row sums,
+        // then the four wave partials in fixed order; each thread then rescales the elements
+        // it summed.
+        const float* wl = xl + n_in;
+        float ss = 0.f;
+        for (uint32_t i = 4 * tid; i < n_in; i += 1024) {
+            const float4v v = *reinterpret_cast<const float4v*>(xl + i);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
+        ss = row16_sum(ss);
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        const float total = (red[0] + red[1]) + (red[2] + red[3]);
+        const float scale = 1.0f / sqrtf(total / float(n_in) + a.eps);
+        for (uint32_t i = 4 * tid; i < n_in; i += 1024) {
+            const float4v v = *reinterpret_cast<const float4v*>(xl + i);
+            const float4v g = *reinterpret_cast<const float4v*>(wl + i);
+            *reinterpret_cast<float4v*>(xl + i) = v * scale * g;
+        }
+        __syncthreads();
+    }
+
     const uint32_t groups = n_in / 8, per_wave = (groups + 3) / 4;
     const uint32_t g_begin = wave * per_wave, g_end = min(groups, g_begin + per_wave);
-    float acc[R];
+    float acc[NR];
 #pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    for (int r = 0; r < NR; r++) acc[r] = 0.f;
     if constexpr (kMvStageW<T>) {
-        const uint8_t* rows = smem + 16 * xchunks + shift;
+        const uint8_t* rows = smem + 16 * (xchunks + achunks) + shift;
         for (uint32_t g = g_begin + lane; g < g_end; g += 64) {
             const float4v x0 = *reinterpret_cast<const float4v*>(xl + 8 * g);
             const float4v x1 = *reinterpret_cast<const float4v*>(xl + 8 * g + 4);
 #pragma unroll
-            for (int r = 0; r < R; r++) {
-                const uint8_t* row = rows + min(uint32_t(r), nrows - 1) * row_bytes;
+            for (int r = 0; r < NR; r++) {
+                const uint8_t* row = rows + (r / R) * 16 * wchunks + min(uint32_t(r % R), nrows - 1) * row_bytes;
                 if constexpr (T == kQ8_0 || T == kQ4_0 || T == kQ4_1) {
                     acc[r] += dot8<T>(row, 8 * g, x0, x1);
                 } else {
@@ -245,19 +323,22 @@ __global__ __launch_bounds__(256) void linear_matvec_kernel(
         }
     } else {
         constexpr uint32_t GB = T == kF32 ? 32 : 16;  // bytes per 8-element group
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(W + start), 0, int(nrows * row_bytes), kBufferFlags);
-        for (uint32_t g = g_begin + lane; g < g_end; g += 64) {
-            u32x4 raw[R][GB / 16];
+        __amdgpu_buffer_rsrc_t rs[NS];
 #pragma unroll
-            for (int r = 0; r < R; r++)
+        for (int s = 0; s < NS; s++)
+            rs[s] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.W[m + s] + start), 0,
+                                                      int(nrows * row_bytes), kBufferFlags);
+        for (uint32_t g = g_begin + lane; g < g_end; g += 64) {
+            u32x4 raw[NR][GB / 16];
+#pragma unroll
+            for (int r = 0; r < NR; r++)
                 for (uint32_t q = 0; q < GB / 16; q++)
                     raw[r][q] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                             rs, int(min(uint32_t(r), nrows - 1) * row_bytes + g * GB + 16 * q), 0, 0));
+                                                             rs[r / R], int(min(uint32_t(r % R), nrows - 1) * row_bytes + g * GB + 16 * q), 0, 0));
             const float4v x0 = *reinterpret_cast<const float4v*>(xl + 8 * g);
             const float4v x1 = *reinterpret_cast<const float4v*>(xl + 8 * g + 4);
 #pragma unroll
-            for (int r = 0; r < R; r++) {
+            for (int r = 0; r < NR; r++) {
                 float w[8];
                 deq8<T>(reinterpret_cast<const uint8_t*>(&raw[r][0]), 0, w);
                 float s = 0.f;
@@ -268,16 +349,380 @@ __global__ __launch_bounds__(256) void linear_matvec_kernel(
         }
     }
 #pragma unroll
-    for (int r = 0; r < R; r++) {
+    for (int r = 0; r < NR; r++) {
         const float s = wave_sum(acc[r]);
-        if (lane == 0) red[wave * R + r] = s;
+        if (lane == 0) red[wave * NR + r] = s;
     }
     __syncthreads();
     if (tid < nrows) {
-        const float s = (red[tid] + red[R + tid]) + (red[2 * R + tid] + red[3 * R + tid]);
-        float* o = out + row0 + tid;
-        *o = accumulate ? *o + s : s;
+        auto total = [&](int r) { return (red[r] + red[NR + r]) + (red[2 * NR + r] + red[3 * NR + r]); };
+        float* o = a.out[m] + row0 + tid;
+        if constexpr (EPI == kEpiSiluGate) {
+            const float g = total(tid), u = total(R + tid);
+            *o = g / (1.0f + expf(-g)) * u;
+        } else {
+            const float s = total(tid);
+            *o = EPI == kEpiAccumulate ? *o + s : s;
+        }
     }
+}
+
+// ---------------------------------------------------------------- one token, streamed rows
+
+// The block types with 32-element blocks and the 16-bit float types take a second one-token
+// kernel that reads weight rows straight from memory into registers (no LDS staging, no
+// barrier between the loads and the arithmetic): x (after the rmsnorm prologue) is staged in
+// LDS once per workgroup; a half-wave (32 lanes) owns RPH rows and walks their 32-element
+// columns, lane l taking columns l, l+32, ..., with the next column's loads issued before the
+// current column's arithmetic. A quantized block is only 2-byte aligned, so a lane loads the
+// dword-aligned window around it (5 dwords for Q4_0 / Q4_1, 9 for Q8_0) and realigns it with
+// v_alignbyte. Each x column is read from LDS once per lane and applied to all RPH rows.
+template <int T> struct Col;
+template <> struct Col<kQ4_0> { static constexpr int ndw = 5, bytes = 18; };
+template <> struct Col<kQ4_1> { static constexpr int ndw = 5, bytes = 20; };
+template <> struct Col<kQ8_0> { static constexpr int ndw = 9, bytes = 34; };
+template <> struct Col<kF16>  { static constexpr int ndw = 16, bytes = 64; };
+template <> struct Col<kBF16> { static constexpr int ndw = 16, bytes = 64; };
+
+template <int T>
+constexpr bool kStreamed = T == kQ4_0 || T == kQ4_1 || T == kQ8_0 || T == kF16 || T == kBF16;
+
+// The window of the column at byte offset off (relative to a 16-byte aligned buffer base).
+template <int T>
+__device__ __forceinline__ void col_load(const __amdgpu_buffer_rsrc_t& rs, uint32_t off, uint32_t (&w)[Col<T>::ndw]) {
+    auto ld4 = [&](uint32_t o, int at) {
+        const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, int(o), 0, 0));
+        w[at] = v[0]; w[at + 1] = v[1]; w[at + 2] = v[2]; w[at + 3] = v[3];
+    };
+    if constexpr (T == kF16 || T == kBF16) {
+        for (int i = 0; i < 4; i++) ld4(off + 16 * i, 4 * i);
+    } else {
+        const uint32_t p = off & ~3u;
+        ld4(p, 0);
+        if constexpr (T == kQ8_0) ld4(p + 16, 4);
+        w[Col<T>::ndw - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(p + 4 * (Col<T>::ndw - 1)), 0, 0);
+    }
+}
+
+__device__ __forceinline__ float dot_u8x4(uint32_t q, const float4v& x) {
+    float s = float(q & 0xFF) * x[0];
+    s = fmaf(float((q >> 8) & 0xFF), x[1], s);
+    s = fmaf(float((q >> 16) & 0xFF), x[2], s);
+    return fmaf(float(q >> 24), x[3], s);
+}
+
+// W-row column · x column (32 elements; sx = sum of the x column, shared by the rows).
+template <int T>
+__device__ __forceinline__ float col_dot(const uint32_t (&w)[Col<T>::ndw], uint32_t off, const float4v (&x)[8], float sx) {
+    if constexpr (T == kF16 || T == kBF16) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+#pragma unroll
+            for (int e = 0; e < 2; e++) {
+                const uint32_t u = w[2 * i + e];
+                float lo, hi;
+                if constexpr (T == kF16) {
+                    lo = f16_bits(u & 0xFFFF);
+                    hi = f16_bits(u >> 16);
+                } else {
+                    lo = __uint_as_float(u << 16);
+                    hi = __uint_as_float(u & 0xFFFF0000u);
+                }
+                s = fmaf(lo, x[i][2 * e], s);
+                s = fmaf(hi, x[i][2 * e + 1], s);
+            }
+        }
+        return s;
+    } else if constexpr (T == kQ4_1) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            s += dot_u8x4(w[1 + i] & 0x0F0F0F0Fu, x[i]);
+            s += dot_u8x4((w[1 + i] >> 4) & 0x0F0F0F0Fu, x[4 + i]);
+        }
+        return fmaf(f16_bits(w[0] & 0xFFFF), s, __fmul_rn(f16_bits(w[0] >> 16), sx));
+    } else {
+        // the block starts at byte 0 or 2 of the window; its quants at byte 2 or 4
+        const bool odd = (off & 2) != 0;
+        const float d = f16_bits((odd ? w[0] >> 16 : w[0]) & 0xFFFF);
+        constexpr int NQ = T == kQ8_0 ? 8 : 4;
+        uint32_t q[NQ];
+#pragma unroll
+        for (int i = 0; i < NQ; i++) q[i] = odd ? w[i + 1] : __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2);
+        float s = 0.f;
+        if constexpr (T == kQ8_0) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) s += dot_u8x4(q[i] ^ 0x80808080u, x[i]);
+            return __fmul_rn(d, fmaf(-128.f, sx, s));
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                s += dot_u8x4(q[i] & 0x0F0F0F0Fu, x[i]);
+                s += dot_u8x4((q[i] >> 4) & 0x0F0F0F0Fu, x[4 + i]);
+            }
+            return __fmul_rn(d, fmaf(-8.f, sx, s));
+        }
+    }
+}
+
+// x chunk (16 bytes) i of the staged x -> its LDS slot: column c = i / 8 keeps its 8 chunks,
+// permuted by (c / 2) % 8, so that the 16 lanes of one LDS read phase (consecutive columns,
+// same chunk) hit 16 different 16-byte bank groups.
+__device__ __forceinline__ uint32_t xslot(uint32_t i) {
+    const uint32_t c = i >> 3;
+    return (c << 3) | ((i & 7) ^ ((c >> 1) & 7));
+}
+
+template <int T, int RPH, int PRO, int EPI>
+__global__ __launch_bounds__(256) void linear_stream_kernel(const MvArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr int NDW = Col<T>::ndw;
+    constexpr int RPM = EPI == kEpiSiluGate ? RPH / 2 : RPH;  // rows of each matrix per half-wave
+    const uint32_t tid = threadIdx.x, lane = tid % 64, hw = tid / 32, l32 = tid % 32;
+    uint32_t m = 0, blk = blockIdx.x;
+    if constexpr (EPI != kEpiSiluGate) {
+        if (blk >= a.blk_end[0]) m = blk >= a.blk_end[1] ? 2 : 1;
+        if (m > 0) blk -= a.blk_end[m - 1];
+    }
+    const uint32_t n_in = a.n_in, row_bytes = a.row_bytes, n_out = a.n_out[m];
+    const uint32_t row0 = blk * 8 * RPM;  // the workgroup's first row of matrix m
+
+    // x (and the norm weights, unpermuted after it) into LDS: all of a thread's loads of a
+    // round are issued before its first LDS store.
+    const uint32_t xchunks = n_in / 4;
+    const uint32_t nchunks = PRO == kProRmsNorm ? 2 * xchunks : xchunks;
+    float4v* xl = reinterpret_cast<float4v*>(smem);
+    {
+        const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0,
+                                                                            int(4 * n_in), kBufferFlags);
+        const __amdgpu_buffer_rsrc_t as = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(PRO == kProRmsNorm ? a.aux : a.x), 0, int(4 * n_in), kBufferFlags);
+        for (uint32_t base = 0; base < nchunks; base += 256 * kMvChunks) {
+            float4v st[kMvChunks];
+#pragma unroll
+            for (int i = 0; i < kMvChunks; i++) {
+                if (base + 256u * i >= nchunks) break;  // workgroup-uniform
+                const uint32_t c = min(base + tid + 256 * i, nchunks - 1);
+                st[i] = __builtin_bit_cast(float4v, c < xchunks
+                    ? __builtin_amdgcn_raw_buffer_load_b128(xs, int(16 * c), 0, 0)
+                    : __builtin_amdgcn_raw_buffer_load_b128(as, int(16 * (c - xchunks)), 0, 0));
+            }
+#pragma unroll
+            for (int i = 0; i < kMvChunks; i++) {
+                if (base + 256u * i >= nchunks) break;
+                const uint32_t c = base + tid + 256 * i;
+                if (c < nchunks) xl[c < xchunks ? xslot(c) : c] = st[i];
+            }
+        }
+    }
+    float* part = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4] wave partials
+    __syncthreads();
+    if constexpr (PRO == kProRmsNorm) {
+        // rmsnorm_kernel's arithmetic and order (float4 per thread strided by 1024 elements,
+        // row sums, the four wave partials in fixed order), then each thread rescales the
+        // chunks it summed.
+        float ss = 0.f;
+        for (uint32_t i = tid; i < xchunks; i += 256) {
+            const float4v v = xl[xslot(i)];
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
+        ss = row16_sum(ss);
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        if (lane == 0) part[tid / 64] = ss;
+        __syncthreads();
+        const float total = (part[0] + part[1]) + (part[2] + part[3]);
+        const float scale = 1.0f / sqrtf(total / float(n_in) + a.eps);
+        for (uint32_t i = tid; i < xchunks; i += 256) xl[xslot(i)] = xl[xslot(i)] * scale * xl[xchunks + i];
+        __syncthreads();
+    }
+
+    // This half-wave's rows: RPM of matrix m (and the same RPM of matrix m + 1 for the gate/up
+    // pair); rows past n_out read the last row and are not written.
+    const uint64_t wbase = (uint64_t(row0) * row_bytes) & ~uint64_t(15);
+    uint32_t roff[RPH];
+#pragma unroll
+    for (int i = 0; i < RPH; i++) {
+        const uint32_t r = min(row0 + hw * RPM + uint32_t(i % RPM), n_out - 1);
+        roff[i] = uint32_t(uint64_t(r) * row_bytes - wbase);
+    }
+    const uint64_t left = (uint64_t(n_out) * row_bytes - wbase + 3) & ~uint64_t(3);
+    const int nrec = int(left < 0x7fffffffu ? left : 0x7fffffffu);
+    __amdgpu_buffer_rsrc_t rs[EPI == kEpiSiluGate ? 2 : 1];
+    rs[0] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.W[m] + wbase), 0, nrec, kBufferFlags);
+    if constexpr (EPI == kEpiSiluGate)
+        rs[1] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.W[1] + wbase), 0, nrec, kBufferFlags);
+
+    const uint32_t ncols = n_in / 32, last = ncols - 1;
+    const uint32_t nsteps = (ncols + 31) / 32;
+    uint32_t b0[RPH][NDW], b1[RPH][NDW];
+    auto load = [&](uint32_t step, uint32_t (&b)[RPH][NDW]) {
+        const uint32_t c = min(step * 32 + l32, last);
+#pragma unroll
+        for (int i = 0; i < RPH; i++) col_load<T>(rs[i / RPM], roff[i] + c * Col<T>::bytes, b[i]);
+    };
+    float acc[RPH];
+#pragma unroll
+    for (int i = 0; i < RPH; i++) acc[i] = 0.f;
+    auto compute = [&](uint32_t step, const uint32_t (&b)[RPH][NDW]) {
+        const uint32_t c0 = step * 32 + l32;
+        const uint32_t c = min(c0, last);
+        float4v xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) xv[j] = xl[(c << 3) | (j ^ ((c >> 1) & 7))];
+        float sx = 0.f;
+        if constexpr (T == kQ4_0 || T == kQ4_1 || T == kQ8_0) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) sx += (xv[j][0] + xv[j][1]) + (xv[j][2] + xv[j][3]);
+        }
+        const bool valid = c0 < ncols;
+#pragma unroll
+        for (int i = 0; i < RPH; i++) {
+            // explicit roundings: every instantiation (rows per half-wave, prologue, epilogue)
+            // sums a row in exactly the same way
+            const float v = col_dot<T>(b[i], roff[i] + c * Col<T>::bytes, xv, sx);
+            acc[i] = __fadd_rn(acc[i], valid ? v : 0.f);
+        }
+    };
+    load(0, b0);
+    for (uint32_t st = 0; st < nsteps; st += 2) {
+        load(st + 1, b1);
+        compute(st, b0);
+        load(st + 2, b0);
+        compute(st + 1, b1);
+    }
+
+    // Row sums over the half-wave; lane i writes row i.
+    float tot[RPH];
+#pragma unroll
+    for (int i = 0; i < RPH; i++) {
+        float t = row16_sum(acc[i]);
+        tot[i] = t + __shfl_xor(t, 16);
+    }
+#pragma unroll
+    for (int i = 0; i < RPM; i++) {
+        const uint32_t r = row0 + hw * RPM + i;
+        if (l32 == uint32_t(i) && r < n_out) {
+            float* o = a.out[m] + r;
+            if constexpr (EPI == kEpiSiluGate) {
+                const float g = tot[i], u = tot[RPM + i];
+                *o = g / (1.0f + expf(-g)) * u;
+            } else {
+                *o = EPI == kEpiAccumulate ? *o + tot[i] : tot[i];
+            }
+        }
+    }
+}
+
+template <int T, int RPH, int PRO, int EPI>
+int launch_st(const MvArgs& a, uint32_t blocks, size_t lds, hipStream_t stream) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&linear_stream_kernel<T, RPH, PRO, EPI>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, int(kMvLdsBytes));
+    if (attr != hipSuccess) return -4;
+    hipLaunchKernelGGL((linear_stream_kernel<T, RPH, PRO, EPI>), dim3(blocks), dim3(256), lds, stream, a);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+template <int T, int RPH, int PRO>
+int launch_st_epi(const MvArgs& a, int epi, uint32_t blocks, size_t lds, hipStream_t stream) {
+    switch (epi) {
+        case kEpiStore: return launch_st<T, RPH, PRO, kEpiStore>(a, blocks, lds, stream);
+        case kEpiAccumulate: return launch_st<T, RPH, PRO, kEpiAccumulate>(a, blocks, lds, stream);
+        default:
+            if constexpr (RPH >= 2) return launch_st<T, RPH, PRO, kEpiSiluGate>(a, blocks, lds, stream);
+            return -2;
+    }
+}
+
+// Rows per half-wave: 4 when that still gives >= 512 workgroups, else 2 when >= 256, else 1
+// (the gate/up pair: 4 or 2, two of each matrix). F16/BF16 windows are 16 dwords: at most 2.
+template <int T>
+int launch_stream_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t stream) {
+    uint32_t rows = 0;
+    for (uint32_t m = 0; m < n_mats; m++) rows += a.n_out[m];
+    constexpr int kMaxRph = T == kF16 || T == kBF16 ? 2 : 4;
+    int rph = rows / 32 >= 512 ? 4 : rows / 16 >= 256 ? 2 : 1;
+    if (rph > kMaxRph) rph = kMaxRph;
+    if (epi == kEpiSiluGate && rph < 2) rph = 2;
+    const int rpm = epi == kEpiSiluGate ? rph / 2 : rph;
+    uint32_t blocks = 0;
+    for (uint32_t m = 0; m < 3; m++) {
+        if (m < n_mats) blocks += (a.n_out[m] + 8 * rpm - 1) / (8 * rpm);
+        a.blk_end[m] = blocks;
+    }
+    if (epi == kEpiSiluGate) blocks = a.blk_end[0];
+    const size_t lds = size_t(a.n_in) * 4 * (pro == kProRmsNorm ? 2 : 1) + 16;
+    if (lds > kMvLdsBytes) return -2;
+    auto go = [&](auto pro_tag) -> int {
+        constexpr int P = decltype(pro_tag)::value;
+        switch (rph) {
+            case 4: if constexpr (kMaxRph >= 4) return launch_st_epi<T, 4, P>(a, epi, blocks, lds, stream); return -2;
+            case 2: return launch_st_epi<T, 2, P>(a, epi, blocks, lds, stream);
+            default: return launch_st_epi<T, 1, P>(a, epi, blocks, lds, stream);
+        }
+    };
+    return pro == kProRmsNorm ? go(std::integral_constant<int, kProRmsNorm>{})
+                              : go(std::integral_constant<int, kProNone>{});
+}
+
+// Bytes of LDS a matvec workgroup stages (x, norm weights, rows) plus its reduction slots.
+template <int T>
+size_t matvec_lds(uint32_t n_in, uint32_t row_bytes, int R, int pro, int epi) {
+    const int ns = epi == kEpiSiluGate ? 2 : 1;
+    const size_t x = size_t(n_in) * 4 * (pro == kProRmsNorm ? 2 : 1);
+    const size_t w = kMvStageW<T> ? (size_t(R) * row_bytes + 15 + 15) / 16 * 16 : 0;
+    return x + ns * w + 4 * size_t(ns) * R * sizeof(float);
+}
+
+template <int T, int R, int PRO, int EPI>
+int launch_mv(const MvArgs& a, uint32_t blocks, size_t lds, hipStream_t stream) {
+    static const hipError_t attr = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&linear_matvec_kernel<T, R, PRO, EPI>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, int(kMvLdsBytes));
+    if (attr != hipSuccess) return -4;
+    hipLaunchKernelGGL((linear_matvec_kernel<T, R, PRO, EPI>), dim3(blocks), dim3(256), lds, stream, a);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+template <int T, int R, int PRO>
+int launch_mv_epi(const MvArgs& a, int epi, uint32_t blocks, size_t lds, hipStream_t stream) {
+    switch (epi) {
+        case kEpiStore: return launch_mv<T, R, PRO, kEpiStore>(a, blocks, lds, stream);
+        case kEpiAccumulate: return launch_mv<T, R, PRO, kEpiAccumulate>(a, blocks, lds, stream);
+        default:
+            if constexpr (R == 4) return launch_mv<T, R, PRO, kEpiSiluGate>(a, blocks, lds, stream);
+            return -2;
+    }
+}
+
+// One token through up to three matrices (n_mats) of type T: out[m] (+)= W[m]·x'.
+template <int T>
+int launch_matvec_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t stream) {
+    const uint32_t n_in = a.n_in;
+    a.row_bytes = n_in / Fmt<T>::blk * Fmt<T>::bytes;
+    if constexpr (kStreamed<T>) return launch_stream_t<T>(a, n_mats, pro, epi, stream);
+    uint32_t rows = 0;
+    for (uint32_t m = 0; m < n_mats; m++) rows = max(rows, a.n_out[m]);
+    // Eight rows per matrix per workgroup when that still leaves >= 3 workgroups per CU
+    // (measured: fewer, larger workgroups are slower here; more rows per workgroup only pay
+    // for x traffic, which is not the limit) and the rows fit the staging buffer; four
+    // otherwise. The gate/up pair takes four of each.
+    int R = 4;
+    if (epi != kEpiSiluGate && rows / 8 >= 768 && matvec_lds<T>(n_in, a.row_bytes, 8, pro, epi) <= kMvLdsBytes) R = 8;
+    const size_t lds = matvec_lds<T>(n_in, a.row_bytes, R, pro, epi);
+    if (lds > kMvLdsBytes) return -2;  // rows too long to stage
+    uint32_t blocks = 0;
+    for (uint32_t m = 0; m < 3; m++) {
+        if (m < n_mats) blocks += (a.n_out[m] + R - 1) / R;
+        a.blk_end[m] = blocks;
+    }
+    if (epi == kEpiSiluGate) blocks = a.blk_end[0];
+    if (pro == kProRmsNorm) return R == 8 ? launch_mv_epi<T, 8, kProRmsNorm>(a, epi, blocks, lds, stream)
+                                          : launch_mv_epi<T, 4, kProRmsNorm>(a, epi, blocks, lds, stream);
+    return R == 8 ? launch_mv_epi<T, 8, kProNone>(a, epi, blocks, lds, stream)
+                  : launch_mv_epi<T, 4, kProNone>(a, epi, blocks, lds, stream);
 }
 
 // ---------------------------------------------------------------- several tokens
@@ -649,36 +1094,20 @@ int launch_t(const uint8_t* W, const float* x, float* out, uint32_t n_in, uint32
              size_t workspace_bytes, hipStream_t stream) {
     const uint32_t row_bytes = n_in / Fmt<T>::blk * Fmt<T>::bytes;
     if (n_tok == 1) {
-        // Eight rows per workgroup when they (and x) fit the staging buffer and the grid still
-        // has >= 3 workgroups per CU; four rows otherwise.
-        const size_t xb = size_t(n_in) * 4;
-        const size_t wrow = kMvStageW<T> ? row_bytes : 0;  // staged bytes per row
-        // Eight rows per workgroup when that still leaves >= 3 workgroups per CU (measured:
-        // fewer, larger workgroups are slower here, more rows per workgroup only pay for x
-        // traffic, which is not the limit), four otherwise.
-        uint32_t R = 4;
-        if (n_out / 8 >= 768 && xb + 8 * wrow + 16 + 4 * 8 * 4 <= kMvLdsBytes) R = 8;
-        if (xb + size_t(R) * wrow + 16 + 4 * R * 4 > kMvLdsBytes) return -2;  // rows too long to stage
-        const uint32_t blocks = (n_out + R - 1) / R;
-        const size_t lds = (xb + size_t(R) * wrow + 16 + 15) / 16 * 16 + 4 * R * sizeof(float);
-        auto launch = [&](auto kernel) {
-            static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                               int(kMvLdsBytes));
-            if (attr != hipSuccess) return -4;
-            hipLaunchKernelGGL(kernel, dim3(blocks), dim3(256), lds, stream, W, x, out, n_in, n_out, row_bytes,
-                               uint64_t(n_out) * row_bytes, accumulate);
-            return 0;
-        };
-        const int rc = R == 8 ? launch(linear_matvec_kernel<T, 8>) : launch(linear_matvec_kernel<T, 4>);
-        if (rc) return rc;
+        MvArgs a{};
+        a.W[0] = W;
+        a.out[0] = out;
+        a.n_out[0] = n_out;
+        a.x = x;
+        a.n_in = n_in;
+        return launch_matvec_t<T>(a, 1, kProNone, accumulate ? kEpiAccumulate : kEpiStore, stream);
     } else {
         const uint32_t tiles_n = (n_out + kMmRows - 1) / kMmRows;
         const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
         uint32_t splits = workspace ? linear_splits(n_in, n_out, n_tok, n_splits, workspace_bytes) : 1;
         // LDS-staged W when rows split into whole 16-byte stage pieces.
         constexpr uint32_t KS = Stage<T>::ks;
-        const bool lw = KS != 0 && row_bytes % 16 == 0 && n_in % KS == 0;
+        const bool lw = KS != 0 && row_bytes % 16 == 0 && n_in % (KS != 0 ? KS : 1) == 0;
         const uint32_t gran = lw ? KS : kMmK;
         const uint32_t units = n_in / gran;
         const uint32_t k_per_split = (units + splits - 1) / splits * gran;
@@ -743,6 +1172,31 @@ size_t linear_workspace_size(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint
     const uint32_t s = linear_splits(n_in, n_out, n_tok, requested, ~size_t(0));
     const uint32_t tiles = ((n_out + kMmRows - 1) / kMmRows) * ((n_tok + kMmToks - 1) / kMmToks);
     return kLinearCounterBytes + (s > 1 ? size_t(tiles) * s * kTileFloats * 4 : 0);
+}
+
+int launch_proj(uint32_t type, const void* const* W, const float* x, const float* aux,
+                float* const* out, uint32_t n_in, const uint32_t* n_out, uint32_t n_mats,
+                int pro, int epi, float eps, hipStream_t stream) {
+    MvArgs a{};
+    for (uint32_t m = 0; m < n_mats; m++) {
+        a.W[m] = static_cast<const uint8_t*>(W[m]);
+        a.n_out[m] = n_out[m];
+        a.out[m] = epi == kEpiSiluGate ? out[0] : out[m];
+    }
+    a.x = x;
+    a.aux = aux;
+    a.n_in = n_in;
+    a.eps = eps;
+    switch (type) {
+        case kF32:  return launch_matvec_t<kF32>(a, n_mats, pro, epi, stream);
+        case kF16:  return launch_matvec_t<kF16>(a, n_mats, pro, epi, stream);
+        case kBF16: return launch_matvec_t<kBF16>(a, n_mats, pro, epi, stream);
+        case kQ8_0: return launch_matvec_t<kQ8_0>(a, n_mats, pro, epi, stream);
+        case kQ4_0: return launch_matvec_t<kQ4_0>(a, n_mats, pro, epi, stream);
+        case kQ4_1: return launch_matvec_t<kQ4_1>(a, n_mats, pro, epi, stream);
+        case kQ6_K: return launch_matvec_t<kQ6_K>(a, n_mats, pro, epi, stream);
+        default:    return -2;
+    }
 }
 
 int launch_linear(uint32_t type, const void* W, const float* x, float* out, uint32_t n_in,

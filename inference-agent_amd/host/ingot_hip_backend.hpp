@@ -10,6 +10,8 @@
 //   embedding rows; per layer: rmsnorm, q/k/v projections, rope(q) + KV store, attention,
 //   x += wo·attn, rmsnorm, gate/up projections, silu(gate)*up, x += down·gate;
 //   rmsnorm of the last token and the logits projection.
+// For one token (decode) rmsnorm + q/k/v, rmsnorm + gate/up + silu and rmsnorm + logits are one
+// ingot_proj launch each (the same results as the separate calls, bit for bit).
 // The model arrives as HostModel, the reference's Model/Layer/Config (src/model.h:8-28) with each
 // gguf::TensorInfo reduced to what the kernels read (type, ne, bytes in the GGUF layout); the
 // weights are copied to the device as they are (no dequantization, no repacking).
@@ -131,22 +133,41 @@ public:
             "embedding");
         for (int l = 0; l < m_.n_layer; l++) {
             const DevLayer& L = layers_[size_t(l)];
-            abi(ingot_rmsnorm(x_, L.attn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
-            linear(L.wq, h_, q_, ne, qd, un, false);
-            linear(L.wk, h_, k_, ne, kvd, un, false);
-            linear(L.wv, h_, v_, ne, kvd, un, false);
+            // One token: rmsnorm + q/k/v in one launch (ingot_proj) when the three share a type.
+            if (n == 1 && L.wq.type == L.wk.type && L.wq.type == L.wv.type) {
+                const Dev* w[3] = {&L.wq, &L.wk, &L.wv};
+                float* outs[3] = {q_, k_, v_};
+                proj(w, 3, x_, L.attn_norm, outs, INGOT_PROJ_RMSNORM, INGOT_PROJ_STORE, "rmsnorm+qkv");
+            } else {
+                abi(ingot_rmsnorm(x_, L.attn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
+                linear(L.wq, h_, q_, ne, qd, un, false);
+                linear(L.wk, h_, k_, ne, kvd, un, false);
+                linear(L.wv, h_, v_, ne, kvd, un, false);
+            }
             attn_->kv_store(l, pos, n, q_, k_, v_);
             attn_->attention(l, pos, n, q_, attn_out_);
             linear(L.wo, attn_out_, x_, qd, ne, un, true);
-            abi(ingot_rmsnorm(x_, L.ffn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
-            linear(L.w_gate, h_, gate_, ne, nf, un, false);
-            linear(L.w_up, h_, up_, ne, nf, un, false);
-            abi(ingot_silu_mul(gate_, up_, uint64_t(n) * nf, stream_), "silu_mul");
+            // One token: rmsnorm + gate/up + silu(gate)*up in one launch.
+            if (n == 1 && L.w_gate.type == L.w_up.type) {
+                const Dev* w[2] = {&L.w_gate, &L.w_up};
+                float* outs[1] = {gate_};
+                proj(w, 2, x_, L.ffn_norm, outs, INGOT_PROJ_RMSNORM, INGOT_PROJ_SILU_GATE, "rmsnorm+gate/up");
+            } else {
+                abi(ingot_rmsnorm(x_, L.ffn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
+                linear(L.w_gate, h_, gate_, ne, nf, un, false);
+                linear(L.w_up, h_, up_, ne, nf, un, false);
+                abi(ingot_silu_mul(gate_, up_, uint64_t(n) * nf, stream_), "silu_mul");
+            }
             linear(L.w_down, gate_, x_, nf, ne, un, true);
         }
-        // Logits only for the last token (src/metal_backend.mm:454-456).
-        abi(ingot_rmsnorm(x_ + size_t(n - 1) * ne, output_norm_, h_, ne, 1, m_.rms_eps, stream_), "rmsnorm");
-        linear(output_, h_, logits_dev_, ne, uint32_t(m_.n_vocab), 1, false);
+        // Logits only for the last token (src/metal_backend.mm:454-456): rmsnorm + output in one
+        // launch.
+        {
+            const Dev* w[1] = {&output_};
+            float* outs[1] = {logits_dev_};
+            proj(w, 1, x_ + size_t(n - 1) * ne, output_norm_, outs, INGOT_PROJ_RMSNORM, INGOT_PROJ_STORE,
+                 "rmsnorm+logits");
+        }
         check(hipMemcpyAsync(logits_.data(), logits_dev_, logits_.size() * sizeof(float), hipMemcpyDeviceToHost,
                              stream_),
               "logits download");
@@ -208,6 +229,23 @@ private:
     static size_t ingot_linear_workspace_size_for(const Dev& w, uint32_t n_tok) {
         IngotLinearDesc d{w.type, w.n_in, w.n_out, n_tok, 0, 0, 0};
         return ingot_linear_workspace_size(&d);
+    }
+    // One token through 1..3 matrices sharing x (ingot_proj).
+    void proj(const Dev* const* w, uint32_t n_mats, const float* x, const float* norm_w, float* const* outs,
+              uint32_t prologue, uint32_t epilogue, const char* what) {
+        IngotProjDesc d{};
+        d.type = w[0]->type;
+        d.n_in = w[0]->n_in;
+        d.n_mats = n_mats;
+        const void* ptrs[3] = {};
+        for (uint32_t m = 0; m < n_mats; m++) {
+            d.n_out[m] = w[m]->n_out;
+            ptrs[m] = w[m]->ptr;
+        }
+        d.prologue = prologue;
+        d.epilogue = epilogue;
+        d.eps = m_.rms_eps;
+        abi(ingot_proj(ptrs, x, norm_w, outs, &d, stream_), what);
     }
     void linear(const Dev& w, const float* x, float* out, uint32_t n_in, uint32_t n_out, uint32_t n, bool acc) {
         IngotLinearDesc d{w.type, n_in, n_out, n, 0, acc ? 1u : 0u, 0};

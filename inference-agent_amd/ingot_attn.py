@@ -32,6 +32,7 @@ EXPORTS = (
     "ingot_linear_splits",
     "ingot_linear_workspace_size",
     "ingot_linear",
+    "ingot_proj",
     "ingot_rmsnorm",
     "ingot_silu_mul",
     "ingot_get_rows",
@@ -102,6 +103,26 @@ class LinearDesc(ctypes.Structure):
     ]
 
 
+# ingot_proj prologues and epilogues (include/ingot_linear.h).
+PROJ_X, PROJ_RMSNORM = 0, 1
+PROJ_STORE, PROJ_ACCUMULATE, PROJ_SILU_GATE = 0, 1, 2
+
+
+class ProjDesc(ctypes.Structure):
+    """IngotProjDesc: one decode token through up to three matrices sharing x, with the
+    rmsnorm before and the residual add / silu gate after fused in."""
+
+    _fields_ = [
+        ("type", c_uint32),
+        ("n_in", c_uint32),
+        ("n_mats", c_uint32),
+        ("n_out", c_uint32 * 3),
+        ("prologue", c_uint32),
+        ("epilogue", c_uint32),
+        ("eps", c_float),
+    ]
+
+
 _lib = None
 
 
@@ -139,6 +160,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ingot_linear_workspace_size.restype = c_size_t
     lib.ingot_linear.argtypes = [c_void_p] * 4 + [c_size_t, ctypes.POINTER(LinearDesc), c_void_p]
     lib.ingot_linear.restype = c_int
+    lib.ingot_proj.argtypes = [ctypes.POINTER(c_void_p), c_void_p, c_void_p, ctypes.POINTER(c_void_p),
+                               ctypes.POINTER(ProjDesc), c_void_p]
+    lib.ingot_proj.restype = c_int
     lib.ingot_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_float, c_void_p]
     lib.ingot_rmsnorm.restype = c_int
     lib.ingot_silu_mul.argtypes = [c_void_p, c_void_p, c_uint64, c_void_p]
@@ -310,6 +334,27 @@ def linear(w, x, out, desc: LinearDesc, stream=None, workspace=None, use_workspa
                           ws, c_size_t(nws), ctypes.byref(desc), _stream_ptr(stream))
     _check(rc, "ingot_linear")
     return out
+
+
+def proj_desc(type_, n_in, n_out, prologue=PROJ_X, epilogue=PROJ_STORE, eps=0.0):
+    t = GGUF_TYPES[type_] if isinstance(type_, str) else int(type_)
+    n_out = list(n_out)
+    return ProjDesc(t, n_in, len(n_out), (c_uint32 * 3)(*(n_out + [0] * (3 - len(n_out)))),
+                    prologue, epilogue, eps)
+
+
+def proj(ws, x, outs, desc: ProjDesc, norm_w=None, stream=None):
+    """One token: out[m] (+)= W[m]·x' for the weight-byte tensors `ws`, x' = x or
+    rmsnorm(x) * norm_w; with PROJ_SILU_GATE (ws = [gate, up]) outs[0] = silu(gate·x') * (up·x').
+    The fused form of rmsnorm + encode_linear (+ encode_silu_mul) (src/metal_backend.mm:433-452)."""
+    n = len(ws)
+    wp = (c_void_p * n)(*[w.data_ptr() for w in ws])
+    op = (c_void_p * len(outs))(*[o.data_ptr() for o in outs])
+    rc = load_library().ingot_proj(wp, c_void_p(x.data_ptr()),
+                                   c_void_p(norm_w.data_ptr() if norm_w is not None else 0), op,
+                                   ctypes.byref(desc), _stream_ptr(stream))
+    _check(rc, "ingot_proj")
+    return outs
 
 
 def rmsnorm(x, w, out, n, n_rows, eps, stream=None):

@@ -4,7 +4,10 @@ class `ingot::HipBackend` (host/ingot_hip_backend.hpp), used by the tests and th
 Follows `MetalBackend::forward_batch` (src/metal_backend.mm:419-471) step by step: embedding
 rows; per layer rmsnorm, q/k/v projections, RoPE + KV-cache store, attention, wo with the
 residual add, rmsnorm, gate/up projections, silu_mul, down with the residual add; the final
-rmsnorm of the last token and the logits projection. Every step is one libingot_attn.so call;
+rmsnorm of the last token and the logits projection. For one token (decode) the rmsnorm and
+the q/k/v projections are one `ingot_proj` launch, as are rmsnorm + gate/up + silu_mul and the
+final rmsnorm + logits (identical results, fewer launches). Every step is one libingot_attn.so
+call;
 PyTorch only holds device memory and the stream. Errors are the reference's
 (src/metal_backend.mm:421-424): "… batch size out of range", "context window exceeded",
 "token id out of range".
@@ -85,11 +88,18 @@ class HipForward:
         ne, qd, kvd, nf = c["n_embd"], self.q_dim, self.kv_dim, c["n_ff"]
         E = self.tok_embd
         ia.get_rows(E[0], E[1], ne, c["n_vocab"], tok, n, self.x)
+        eps = c["rms_eps"]
         for l, L in enumerate(self.layers):
-            ia.rmsnorm(self.x, L["attn_norm"], self.h, ne, n, c["rms_eps"])
-            self._lin(L["wq"], self.h, self.q, ne, qd, n)
-            self._lin(L["wk"], self.h, self.k, ne, kvd, n)
-            self._lin(L["wv"], self.h, self.v, ne, kvd, n)
+            qkv_fused = n == 1 and L["wq"][0] == L["wk"][0] == L["wv"][0]
+            if qkv_fused:
+                ia.proj([L["wq"][1], L["wk"][1], L["wv"][1]], self.x, [self.q, self.k, self.v],
+                        ia.proj_desc(L["wq"][0], ne, [qd, kvd, kvd], prologue=ia.PROJ_RMSNORM, eps=eps),
+                        norm_w=L["attn_norm"])
+            else:
+                ia.rmsnorm(self.x, L["attn_norm"], self.h, ne, n, eps)
+                self._lin(L["wq"], self.h, self.q, ne, qd, n)
+                self._lin(L["wk"], self.h, self.k, ne, kvd, n)
+                self._lin(L["wv"], self.h, self.v, ne, kvd, n)
             ia.rope_kv_store(self.q, self.k, self.v, self.k_cache, self.v_cache, self.inv_freq,
                              ia.rope_kv_desc(c["n_head"], c["n_head_kv"], c["head_dim"], pos, n,
                                              dst_offset=(l * self.n_ctx + pos) * kvd))
@@ -103,16 +113,23 @@ class HipForward:
                                 ia.prefill_desc(c["n_head"], c["n_head_kv"], c["head_dim"], pos, n,
                                                 kv_offset=kv_offset, scale=self.scale), workspace=self.attn_ws)
             self._lin(L["wo"], self.attn, self.x, qd, ne, n, acc=True)
-            ia.rmsnorm(self.x, L["ffn_norm"], self.h, ne, n, c["rms_eps"])
-            self._lin(L["w_gate"], self.h, self.gate, ne, nf, n)
-            self._lin(L["w_up"], self.h, self.up, ne, nf, n)
-            ia.silu_mul(self.gate, self.up, n * nf)
+            if n == 1 and L["w_gate"][0] == L["w_up"][0]:
+                ia.proj([L["w_gate"][1], L["w_up"][1]], self.x, [self.gate],
+                        ia.proj_desc(L["w_gate"][0], ne, [nf, nf], prologue=ia.PROJ_RMSNORM,
+                                     epilogue=ia.PROJ_SILU_GATE, eps=eps),
+                        norm_w=L["ffn_norm"])
+            else:
+                ia.rmsnorm(self.x, L["ffn_norm"], self.h, ne, n, eps)
+                self._lin(L["w_gate"], self.h, self.gate, ne, nf, n)
+                self._lin(L["w_up"], self.h, self.up, ne, nf, n)
+                ia.silu_mul(self.gate, self.up, n * nf)
             self._lin(L["w_down"], self.gate, self.x, nf, ne, n, acc=True)
         # logits for the last token only (src/metal_backend.mm:454-456)
         last = self.x[n - 1:n]
-        ia.rmsnorm(last, self.output_norm, self.h, ne, 1, c["rms_eps"])
         O = self.output
-        self._lin(O, self.h, self.logits, ne, c["n_vocab"], 1)
+        ia.proj([O[1]], last, [self.logits],
+                ia.proj_desc(O[0], ne, [c["n_vocab"]], prologue=ia.PROJ_RMSNORM, eps=eps),
+                norm_w=self.output_norm)
         return self.logits
 
     def forward(self, token: int, pos: int):

@@ -71,6 +71,10 @@ def test_struct_layout_matches_c():
                offsetof(IngotRopeKvDesc, q_stride), offsetof(IngotRopeKvDesc, kv_stride));
         printf("%zu %zu %zu\n", sizeof(IngotLinearDesc), offsetof(IngotLinearDesc, accumulate),
                offsetof(IngotLinearDesc, n_splits));
+        printf("%zu %zu %zu %zu\n", sizeof(IngotProjDesc), offsetof(IngotProjDesc, n_out),
+               offsetof(IngotProjDesc, epilogue), offsetof(IngotProjDesc, eps));
+        printf("%d %d %d %d %d\n", INGOT_PROJ_X, INGOT_PROJ_RMSNORM, INGOT_PROJ_STORE,
+               INGOT_PROJ_ACCUMULATE, INGOT_PROJ_SILU_GATE);
         return 0;
     }
     """
@@ -81,11 +85,13 @@ def test_struct_layout_matches_c():
         subprocess.run(["gcc", "-I", INCLUDE, c, "-o", exe], check=True)
         vals = [int(x) for x in subprocess.run([exe], capture_output=True, text=True).stdout.split()]
     D, P, R = ingot_attn.DecodeDesc, ingot_attn.PrefillDesc, ingot_attn.RopeKvDesc
-    Li = ingot_attn.LinearDesc
+    Li, Pj = ingot_attn.LinearDesc, ingot_attn.ProjDesc
     assert vals == [ctypes.sizeof(D), D.kv_offset.offset, D.scale.offset, ctypes.sizeof(P),
                     P.kv_offset.offset, P.q_stride.offset, P.scale.offset, ctypes.sizeof(R),
                     R.dst_offset.offset, R.q_stride.offset, R.kv_stride.offset, ctypes.sizeof(Li),
-                    Li.accumulate.offset, Li.n_splits.offset]
+                    Li.accumulate.offset, Li.n_splits.offset, ctypes.sizeof(Pj), Pj.n_out.offset,
+                    Pj.epilogue.offset, Pj.eps.offset, ingot_attn.PROJ_X, ingot_attn.PROJ_RMSNORM,
+                    ingot_attn.PROJ_STORE, ingot_attn.PROJ_ACCUMULATE, ingot_attn.PROJ_SILU_GATE]
 
 
 def test_host_validation(lib):
@@ -179,3 +185,35 @@ def test_linear_descriptor_checks(lib):
     assert lib.ingot_linear(P((1 << 20) + 8), a, a, None, 0, ctypes.byref(d), None) == -1  # w align
     assert lib.ingot_linear(a, a, P((1 << 20) + 2), None, 0, ctypes.byref(d), None) == -1  # out align
     assert lib.ingot_linear(a, a, a, None, 0, None, None) == -1
+
+
+def test_proj_descriptor_checks(lib):
+    """Argument checks of the fused one-token projection (no compute call: every case is
+    rejected before a launch)."""
+    import ingot_attn as ia
+
+    P = ctypes.c_void_p
+    a = P(1 << 20)
+    arr = lambda *ps: (ctypes.c_void_p * len(ps))(*ps)
+    call = lambda d, w=None, x=a, nw=a, out=None: lib.ingot_proj(
+        w if w is not None else arr(a, a, a), x, nw, out if out is not None else arr(a, a, a),
+        ctypes.byref(d) if d is not None else None, None)
+    assert call(None) == -1
+    assert call(ia.proj_desc("Q4_0", 3072, [])) == -1                      # no matrix
+    bad = ia.proj_desc("Q4_0", 3072, [8, 8, 8]); bad.n_mats = 4
+    assert call(bad) == -1                                                 # more than three
+    assert call(ia.proj_desc(6, 256, [4])) == -2                           # Q5_0: no kernel
+    assert call(ia.proj_desc("Q6_K", 128, [4])) == -2                      # n_in % 256
+    assert call(ia.proj_desc("F16", 48, [4])) == -2                        # n_in % 32
+    assert call(ia.proj_desc("F16", 256, [4], prologue=2)) == -1
+    assert call(ia.proj_desc("F16", 256, [4], epilogue=3)) == -1
+    assert call(ia.proj_desc("F16", 256, [4, 0])) == -1                    # empty matrix
+    assert call(ia.proj_desc("F16", 256, [4]), x=P((1 << 20) + 4)) == -1   # x align
+    assert call(ia.proj_desc("F16", 256, [4]), w=arr(P((1 << 20) + 8))) == -1
+    assert call(ia.proj_desc("F16", 256, [4]), out=arr(P((1 << 20) + 2))) == -1
+    assert call(ia.proj_desc("F16", 256, [4], prologue=1), nw=None) == -1  # rmsnorm weights
+    assert call(ia.proj_desc("F16", 256, [4], prologue=1, eps=-1.0)) == -1
+    # the silu gate takes exactly (gate, up) of equal length
+    assert call(ia.proj_desc("F16", 256, [4], epilogue=2)) == -1
+    assert call(ia.proj_desc("F16", 256, [4, 8], epilogue=2)) == -1
+    assert call(ia.proj_desc("F16", 256, [4, 4, 4], epilogue=2)) == -1

@@ -76,7 +76,8 @@ def _x(n_tok, n_in, seed):
 
 
 @pytest.mark.parametrize("t", TYPES)
-@pytest.mark.parametrize("n_in,n_out", [(3072, 3072), (256, 200), (8192, 96), (512, 1001)])
+@pytest.mark.parametrize("n_in,n_out", [(3072, 3072), (256, 200), (8192, 96), (512, 1001), (256, 1001),
+                                         (768, 3)])
 def test_matvec(dev, oracle_mod, t, n_in, n_out):
     raw = gb.random_weights(t, n_out, n_in, seed=n_in + n_out)
     x = _x(1, n_in, seed=1)

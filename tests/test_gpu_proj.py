@@ -1,0 +1,154 @@
+"""GPU parity of the fused one-token projection (ingot_proj) — the rmsnorm before q/k/v and
+gate/up, up to three matrices in one launch, the residual accumulate and the silu gate after.
+
+Two bars, stated per test:
+  - against the unfused library sequence (ingot_rmsnorm, ingot_linear with n_tok = 1,
+    ingot_silu_mul): bit-exact — the fused kernel performs the same f32 operations in the same
+    order;
+  - against the CPU oracle (ops::rmsnorm, ops::matvec, silu(gate)*up): rel-L2 <= 1e-5 and
+    max|d| <= 1e-5 * max|ref| + 1e-6, the bar of the linear layer's one-token path (the order of
+    the f32 sums differs, and the GPU's expf in the silu).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import ensure_built
+
+import gguf_blocks as gb
+
+pytestmark = pytest.mark.gpu
+
+TYPES = ["F32", "F16", "BF16", "Q8_0", "Q4_0", "Q4_1", "Q6_K"]
+EPS = 1e-5
+
+
+@pytest.fixture(scope="module")
+def dev():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.fail("GPU test run without a GPU")
+    ensure_built("lib")
+    import ingot_attn
+
+    ingot_attn.load_library()
+    return torch.device("cuda:0")
+
+
+def _t(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _close(got, want, what):
+    d = np.abs(got.astype(np.float64) - want)
+    rel = np.linalg.norm(got - want) / max(np.linalg.norm(want), 1e-30)
+    tol = 1e-5 * np.abs(want).max() + 1e-6
+    assert np.all(np.isfinite(got)), f"{what}: non-finite output"
+    assert d.max() <= tol and rel <= 1e-5, f"{what}: max|d|={d.max():.3e} (tol {tol:.1e}), rel-L2={rel:.3e}"
+
+
+def _inputs(t, n_in, n_outs, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal((1, n_in)) * 2).astype(np.float32)
+    nw = (1 + 0.3 * rng.standard_normal(n_in)).astype(np.float32)
+    raws = [gb.random_weights(t, n, n_in, seed=seed + 10 * i + 1) for i, n in enumerate(n_outs)]
+    return x, nw, raws
+
+
+def _unfused(dev, t, raws, x, nw, n_in, n_outs, rms, base=None):
+    """The same step as separate library calls: rmsnorm, one ingot_linear per matrix."""
+    import torch
+    import ingot_attn as ia
+
+    xd = _t(x, dev)
+    h = torch.empty_like(xd)
+    if rms:
+        ia.rmsnorm(xd, _t(nw, dev), h, n_in, 1, EPS)
+    else:
+        h = xd
+    outs = []
+    for i, (raw, n) in enumerate(zip(raws, n_outs)):
+        out = _t(base[i] if base is not None else np.zeros((1, n), np.float32), dev)
+        ia.linear(_t(raw.reshape(-1), dev), h, out, ia.linear_desc(t, n_in, n, 1, accumulate=base is not None),
+                  use_workspace=False)
+        outs.append(out)
+    torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in,n_outs", [(3072, (3072, 1024, 1024)), (512, (200, 77, 3)), (256, (1001,))])
+def test_rmsnorm_qkv(dev, oracle_mod, t, n_in, n_outs):
+    import torch
+    import ingot_attn as ia
+
+    x, nw, raws = _inputs(t, n_in, n_outs, seed=n_in + len(n_outs))
+    outs = [_t(np.full((1, n), np.nan, np.float32), dev) for n in n_outs]
+    d = ia.proj_desc(t, n_in, n_outs, prologue=ia.PROJ_RMSNORM, eps=EPS)
+    ia.proj([_t(r.reshape(-1), dev) for r in raws], _t(x, dev), outs, d, norm_w=_t(nw, dev))
+    torch.cuda.synchronize()
+    ref = _unfused(dev, t, raws, x, nw, n_in, n_outs, rms=True)
+    h = oracle_mod.rmsnorm(x, nw, EPS)
+    for i, (o, r, raw, n) in enumerate(zip(outs, ref, raws, n_outs)):
+        got = o.cpu().numpy()
+        assert np.array_equal(got, r.cpu().numpy()), f"{t} matrix {i}: fused != rmsnorm + ingot_linear"
+        _close(got, oracle_mod.linear(t, raw, h, n_in, n), f"{t} {n_in}x{n} matrix {i}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in,n_ff", [(3072, 8192), (512, 1000), (256, 5)])
+def test_rmsnorm_gate_up_silu(dev, oracle_mod, t, n_in, n_ff):
+    import torch
+    import ingot_attn as ia
+
+    x, nw, raws = _inputs(t, n_in, (n_ff, n_ff), seed=7 + n_ff)
+    out = _t(np.full((1, n_ff), np.nan, np.float32), dev)
+    d = ia.proj_desc(t, n_in, [n_ff, n_ff], prologue=ia.PROJ_RMSNORM, epilogue=ia.PROJ_SILU_GATE, eps=EPS)
+    ia.proj([_t(r.reshape(-1), dev) for r in raws], _t(x, dev), [out], d, norm_w=_t(nw, dev))
+    torch.cuda.synchronize()
+    g, u = _unfused(dev, t, raws, x, nw, n_in, (n_ff, n_ff), rms=True)
+    ia.silu_mul(g, u, n_ff) if n_ff % 4 == 0 else None
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    if n_ff % 4 == 0:  # ingot_silu_mul takes multiples of 4
+        assert np.array_equal(got, g.cpu().numpy()), f"{t}: fused != rmsnorm + linear x2 + silu_mul"
+    h = oracle_mod.rmsnorm(x, nw, EPS)
+    want = oracle_mod.silu_mul(oracle_mod.linear(t, raws[0], h, n_in, n_ff),
+                               oracle_mod.linear(t, raws[1], h, n_in, n_ff))
+    _close(got, want, f"{t} gate/up {n_in}x{n_ff}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_in,n_out", [(3072, 3072), (8192, 3072), (512, 37)])
+def test_accumulate(dev, oracle_mod, t, n_in, n_out):
+    """wo / w_down: out += W·x, no prologue."""
+    import torch
+    import ingot_attn as ia
+
+    x, nw, raws = _inputs(t, n_in, (n_out,), seed=3 + n_in)
+    base = np.random.default_rng(9).standard_normal((1, n_out)).astype(np.float32)
+    out = _t(base, dev)
+    ia.proj([_t(raws[0].reshape(-1), dev)], _t(x, dev), [out],
+            ia.proj_desc(t, n_in, [n_out], epilogue=ia.PROJ_ACCUMULATE))
+    torch.cuda.synchronize()
+    ref = _unfused(dev, t, raws, x, nw, n_in, (n_out,), rms=False, base=[base])[0]
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref.cpu().numpy()), f"{t}: fused != ingot_linear accumulate"
+    _close(got, base + oracle_mod.linear(t, raws[0], x, n_in, n_out), f"{t} accumulate {n_in}x{n_out}")
+
+
+def test_rows_too_long(dev):
+    """Rows whose staging exceeds the 160 KB of LDS are refused, not truncated."""
+    import torch
+    import ingot_attn as ia
+
+    n_in = 32768  # x alone is 128 KB; with the rmsnorm weights 256 KB
+    w = torch.zeros(n_in // 32 * 18 * 4, dtype=torch.uint8, device=dev)
+    x = torch.zeros(n_in, device=dev)
+    out = torch.zeros(4, device=dev)
+    with pytest.raises(RuntimeError):
+        ia.proj([w], x, [out], ia.proj_desc("Q4_0", n_in, [4], prologue=ia.PROJ_RMSNORM, eps=EPS), norm_w=x)
