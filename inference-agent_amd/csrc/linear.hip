@@ -242,29 +242,39 @@ __global__ __launch_bounds__(256) void linear_matvec_kernel(const MvArgs a) {
                                                                         int(4 * n_in), kBufferFlags);
     const __amdgpu_buffer_rsrc_t as = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(PRO == kProRmsNorm ? a.aux : a.x), 0, int(4 * n_in), kBufferFlags);
-    for (uint32_t base = 0; base < nchunks; base += 256 * kMvChunks) {
+    // The staging rounds walk the regions x | norm weights | row set 0 | row set 1, each padded
+    // to a multiple of 256 chunks, so that a load's source (its buffer descriptor) is uniform
+    // across the workgroup: a descriptor chosen per lane makes the compiler loop over the
+    // distinct descriptors of a wave.
+    const uint32_t px = (xchunks + 255) & ~255u, pa = (achunks + 255) & ~255u, pw = (wchunks + 255) & ~255u;
+    const uint32_t nvirt = px + pa + NS * pw;
+    for (uint32_t base = 0; base < nvirt; base += 256 * kMvChunks) {
         u32x4 st[kMvChunks];
+        uint32_t dst[kMvChunks];
 #pragma unroll
         for (int i = 0; i < kMvChunks; i++) {
-            if (base + 256u * i >= nchunks) break;  // workgroup-uniform: only chunks that exist
-            const uint32_t c = min(base + tid + 256 * i, nchunks - 1);
-            if (c < xchunks) {
-                st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xs, int(16 * c), 0, 0));
-            } else if (PRO == kProRmsNorm && c < xchunks + achunks) {
-                st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(as, int(16 * (c - xchunks)), 0, 0));
+            const uint32_t v0 = base + 256u * i;  // workgroup-uniform
+            if (v0 >= nvirt) break;
+            // region of this round slot, its chunk count, LDS chunk offset and descriptor
+            uint32_t start, count, lds0;
+            __amdgpu_buffer_rsrc_t src;
+            if (v0 < px) {
+                start = 0; count = xchunks; lds0 = 0; src = xs;
+            } else if (v0 < px + pa) {
+                start = px; count = achunks; lds0 = xchunks; src = as;
+            } else if (NS == 1 || v0 < px + pa + pw) {
+                start = px + pa; count = wchunks; lds0 = xchunks + achunks; src = ws[0];
             } else {
-                const uint32_t cw = c - xchunks - achunks;
-                if (NS == 2 && cw >= wchunks)
-                    st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ws[NS - 1], int(16 * (cw - wchunks)), 0, 0));
-                else
-                    st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(ws[0], int(16 * cw), 0, 0));
+                start = px + pa + pw; count = wchunks; lds0 = xchunks + achunks + wchunks; src = ws[NS - 1];
             }
+            const uint32_t local = v0 - start + tid;
+            st[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(src, int(16 * min(local, count - 1)), 0, 0));
+            dst[i] = local < count ? lds0 + local : ~0u;
         }
 #pragma unroll
         for (int i = 0; i < kMvChunks; i++) {
-            const uint32_t c = base + tid + 256 * i;
-            if (base + 256u * i >= nchunks) break;
-            if (c < nchunks) *reinterpret_cast<u32x4*>(smem + 16 * c) = st[i];
+            if (base + 256u * i >= nvirt) break;
+            if (dst[i] != ~0u) *reinterpret_cast<u32x4*>(smem + 16 * dst[i]) = st[i];
         }
     }
     float* red = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4 waves][NR]
@@ -404,11 +414,26 @@ __device__ __forceinline__ void col_load(const __amdgpu_buffer_rsrc_t& rs, uint3
     }
 }
 
-__device__ __forceinline__ float dot_u8x4(uint32_t q, const float4v& x) {
-    float s = float(q & 0xFF) * x[0];
+// s + sum_k byte_k(q) * x[k], one fma per element (v_cvt_f32_ubyte0..3 read the bytes in place).
+__device__ __forceinline__ float fma_u8x4(uint32_t q, const float4v& x, float s) {
+    s = fmaf(float(q & 0xFF), x[0], s);
     s = fmaf(float((q >> 8) & 0xFF), x[1], s);
     s = fmaf(float((q >> 16) & 0xFF), x[2], s);
     return fmaf(float(q >> 24), x[3], s);
+}
+
+// The low / high nibbles of each byte of w, as bytes. The mask is applied in inline asm so the
+// optimizer cannot fold it into the byte extraction of fma_u8x4 (it would turn each
+// v_cvt_f32_ubyteN into a bit-field extract plus a conversion).
+__device__ __forceinline__ uint32_t lo_nibbles(uint32_t w) {
+    uint32_t r;
+    asm("v_and_b32 %0, 0x0f0f0f0f, %1" : "=v"(r) : "v"(w));
+    return r;
+}
+__device__ __forceinline__ uint32_t hi_nibbles(uint32_t w) {
+    uint32_t r;
+    asm("v_lshrrev_b32 %0, 4, %1\n\tv_and_b32 %0, 0x0f0f0f0f, %0" : "=&v"(r) : "v"(w));
+    return r;
 }
 
 // W-row column · x column (32 elements; sx = sum of the x column, shared by the rows).
@@ -438,8 +463,8 @@ __device__ __forceinline__ float col_dot(const uint32_t (&w)[Col<T>::ndw], uint3
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            s += dot_u8x4(w[1 + i] & 0x0F0F0F0Fu, x[i]);
-            s += dot_u8x4((w[1 + i] >> 4) & 0x0F0F0F0Fu, x[4 + i]);
+            s = fma_u8x4(lo_nibbles(w[1 + i]), x[i], s);
+            s = fma_u8x4(hi_nibbles(w[1 + i]), x[4 + i], s);
         }
         return fmaf(f16_bits(w[0] & 0xFFFF), s, __fmul_rn(f16_bits(w[0] >> 16), sx));
     } else {
@@ -453,13 +478,13 @@ __device__ __forceinline__ float col_dot(const uint32_t (&w)[Col<T>::ndw], uint3
         float s = 0.f;
         if constexpr (T == kQ8_0) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) s += dot_u8x4(q[i] ^ 0x80808080u, x[i]);
+            for (int i = 0; i < 8; i++) s = fma_u8x4(q[i] ^ 0x80808080u, x[i], s);
             return __fmul_rn(d, fmaf(-128.f, sx, s));
         } else {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                s += dot_u8x4(q[i] & 0x0F0F0F0Fu, x[i]);
-                s += dot_u8x4((q[i] >> 4) & 0x0F0F0F0Fu, x[4 + i]);
+                s = fma_u8x4(lo_nibbles(q[i]), x[i], s);
+                s = fma_u8x4(hi_nibbles(q[i]), x[4 + i], s);
             }
             return __fmul_rn(d, fmaf(-8.f, sx, s));
         }
@@ -474,8 +499,8 @@ __device__ __forceinline__ uint32_t xslot(uint32_t i) {
     return (c << 3) | ((i & 7) ^ ((c >> 1) & 7));
 }
 
-template <int T, int RPH, int PRO, int EPI>
-__global__ __launch_bounds__(256) void linear_stream_kernel(const MvArgs a) {
+template <int T, int RPH, int PRO, int EPI, int NT>
+__global__ __launch_bounds__(NT) void linear_stream_kernel(const MvArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     constexpr int NDW = Col<T>::ndw;
     constexpr int RPM = EPI == kEpiSiluGate ? RPH / 2 : RPH;  // rows of each matrix per half-wave
@@ -486,57 +511,8 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const MvArgs a) {
         if (m > 0) blk -= a.blk_end[m - 1];
     }
     const uint32_t n_in = a.n_in, row_bytes = a.row_bytes, n_out = a.n_out[m];
-    const uint32_t row0 = blk * 8 * RPM;  // the workgroup's first row of matrix m
-
-    // x (and the norm weights, unpermuted after it) into LDS: all of a thread's loads of a
-    // round are issued before its first LDS store.
-    const uint32_t xchunks = n_in / 4;
-    const uint32_t nchunks = PRO == kProRmsNorm ? 2 * xchunks : xchunks;
-    float4v* xl = reinterpret_cast<float4v*>(smem);
-    {
-        const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0,
-                                                                            int(4 * n_in), kBufferFlags);
-        const __amdgpu_buffer_rsrc_t as = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(PRO == kProRmsNorm ? a.aux : a.x), 0, int(4 * n_in), kBufferFlags);
-        for (uint32_t base = 0; base < nchunks; base += 256 * kMvChunks) {
-            float4v st[kMvChunks];
-#pragma unroll
-            for (int i = 0; i < kMvChunks; i++) {
-                if (base + 256u * i >= nchunks) break;  // workgroup-uniform
-                const uint32_t c = min(base + tid + 256 * i, nchunks - 1);
-                st[i] = __builtin_bit_cast(float4v, c < xchunks
-                    ? __builtin_amdgcn_raw_buffer_load_b128(xs, int(16 * c), 0, 0)
-                    : __builtin_amdgcn_raw_buffer_load_b128(as, int(16 * (c - xchunks)), 0, 0));
-            }
-#pragma unroll
-            for (int i = 0; i < kMvChunks; i++) {
-                if (base + 256u * i >= nchunks) break;
-                const uint32_t c = base + tid + 256 * i;
-                if (c < nchunks) xl[c < xchunks ? xslot(c) : c] = st[i];
-            }
-        }
-    }
-    float* part = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4] wave partials
-    __syncthreads();
-    if constexpr (PRO == kProRmsNorm) {
-        // rmsnorm_kernel's arithmetic and order (float4 per thread strided by 1024 elements,
-        // row sums, the four wave partials in fixed order), then each thread rescales the
-        // chunks it summed.
-        float ss = 0.f;
-        for (uint32_t i = tid; i < xchunks; i += 256) {
-            const float4v v = xl[xslot(i)];
-            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-        }
-        ss = row16_sum(ss);
-        ss += __shfl_xor(ss, 16);
-        ss += __shfl_xor(ss, 32);
-        if (lane == 0) part[tid / 64] = ss;
-        __syncthreads();
-        const float total = (part[0] + part[1]) + (part[2] + part[3]);
-        const float scale = 1.0f / sqrtf(total / float(n_in) + a.eps);
-        for (uint32_t i = tid; i < xchunks; i += 256) xl[xslot(i)] = xl[xslot(i)] * scale * xl[xchunks + i];
-        __syncthreads();
-    }
+    constexpr uint32_t NHW = NT / 32;  // half-waves
+    const uint32_t row0 = blk * NHW * RPM;  // the workgroup's first row of matrix m
 
     // This half-wave's rows: RPM of matrix m (and the same RPM of matrix m + 1 for the gate/up
     // pair); rows past n_out read the last row and are not written.
@@ -556,12 +532,82 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const MvArgs a) {
 
     const uint32_t ncols = n_in / 32, last = ncols - 1;
     const uint32_t nsteps = (ncols + 31) / 32;
-    uint32_t b0[RPH][NDW], b1[RPH][NDW];
+    uint32_t b0[RPH][NDW], b1[RPH][NDW], b2[RPH][NDW];
     auto load = [&](uint32_t step, uint32_t (&b)[RPH][NDW]) {
         const uint32_t c = min(step * 32 + l32, last);
 #pragma unroll
         for (int i = 0; i < RPH; i++) col_load<T>(rs[i / RPM], roff[i] + c * Col<T>::bytes, b[i]);
     };
+    // x (and the norm weights, unpermuted after it) into LDS. The loads of x's first round go
+    // out first, then the first three columns of the rows (they do not depend on x), then x is
+    // stored: the row data streams in while x is staged and normalized.
+    const uint32_t xchunks = n_in / 4;
+    const uint32_t nchunks = PRO == kProRmsNorm ? 2 * xchunks : xchunks;
+    float4v* xl = reinterpret_cast<float4v*>(smem);
+    const __amdgpu_buffer_rsrc_t xs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0,
+                                                                        int(4 * n_in), kBufferFlags);
+    const __amdgpu_buffer_rsrc_t as = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(PRO == kProRmsNorm ? a.aux : a.x), 0, int(4 * n_in), kBufferFlags);
+    auto stage_round = [&](uint32_t base, bool prefetch) {
+        float4v st[kMvChunks];
+        // (x chunks and norm-weight chunks come from two descriptors; the choice is made per
+        // load from the workgroup-uniform round position, never per lane, which would make the
+        // compiler loop over the distinct descriptors of a wave)
+#pragma unroll
+        for (int i = 0; i < kMvChunks; i++) {
+            if (base + NT * i >= nchunks) break;  // workgroup-uniform
+            const uint32_t c = min(base + tid + NT * i, nchunks - 1);
+            const uint32_t cx = min(c, xchunks - 1);
+            const float4v vx = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(xs, int(16 * cx), 0, 0));
+            if (PRO == kProRmsNorm && base + NT * i + NT - 1 >= xchunks) {
+                const uint32_t ca = c >= xchunks ? c - xchunks : 0;
+                const float4v va = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(as, int(16 * ca), 0, 0));
+                st[i] = c < xchunks ? vx : va;
+            } else {
+                st[i] = vx;
+            }
+        }
+        if (prefetch) {
+            load(0, b0);
+            load(1, b1);
+            load(2, b2);
+        }
+#pragma unroll
+        for (int i = 0; i < kMvChunks; i++) {
+            if (base + NT * i >= nchunks) break;
+            const uint32_t c = base + tid + NT * i;
+            if (c < nchunks) xl[c < xchunks ? xslot(c) : c] = st[i];
+        }
+    };
+    stage_round(0, false);
+    for (uint32_t base = NT * kMvChunks; base < nchunks; base += NT * kMvChunks) stage_round(base, false);
+    float* part = reinterpret_cast<float*>(smem + 16 * nchunks);  // [4] wave partials
+    __syncthreads();
+    load(0, b0);
+    load(1, b1);
+    load(2, b2);
+    if constexpr (PRO == kProRmsNorm) {
+        // rmsnorm_kernel's arithmetic and order: its 256 threads' float4 sums strided by 1024
+        // elements (the first four waves here), row sums, the four wave partials in fixed
+        // order; then the elementwise rescale by every thread.
+        if (tid < 256) {
+            float ss = 0.f;
+            for (uint32_t i = tid; i < xchunks; i += 256) {
+                const float4v v = xl[xslot(i)];
+                ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+            }
+            ss = row16_sum(ss);
+            ss += __shfl_xor(ss, 16);
+            ss += __shfl_xor(ss, 32);
+            if (lane == 0) part[tid / 64] = ss;
+        }
+        __syncthreads();
+        const float total = (part[0] + part[1]) + (part[2] + part[3]);
+        const float scale = 1.0f / sqrtf(total / float(n_in) + a.eps);
+        for (uint32_t i = tid; i < xchunks; i += NT) xl[xslot(i)] = xl[xslot(i)] * scale * xl[xchunks + i];
+        __syncthreads();
+    }
+
     float acc[RPH];
 #pragma unroll
     for (int i = 0; i < RPH; i++) acc[i] = 0.f;
@@ -585,13 +631,20 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const MvArgs a) {
             acc[i] = __fadd_rn(acc[i], valid ? v : 0.f);
         }
     };
-    load(0, b0);
-    for (uint32_t st = 0; st < nsteps; st += 2) {
-        load(st + 1, b1);
+    // three columns in flight (all of a 3072-long row), refilled as each is computed; the
+    // last three buffered columns are computed without refills
+    uint32_t st = 0;
+    for (; st + 3 < nsteps; st += 3) {
         compute(st, b0);
-        load(st + 2, b0);
+        load(st + 3, b0);
         compute(st + 1, b1);
+        load(st + 4, b1);
+        compute(st + 2, b2);
+        load(st + 5, b2);
     }
+    compute(st, b0);
+    compute(st + 1, b1);
+    compute(st + 2, b2);
 
     // Row sums over the half-wave; lane i writes row i.
     float tot[RPH];
@@ -615,56 +668,72 @@ __global__ __launch_bounds__(256) void linear_stream_kernel(const MvArgs a) {
     }
 }
 
-template <int T, int RPH, int PRO, int EPI>
+template <int T, int RPH, int PRO, int EPI, int NT>
 int launch_st(const MvArgs& a, uint32_t blocks, size_t lds, hipStream_t stream) {
     static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&linear_stream_kernel<T, RPH, PRO, EPI>),
+        reinterpret_cast<const void*>(&linear_stream_kernel<T, RPH, PRO, EPI, NT>),
         hipFuncAttributeMaxDynamicSharedMemorySize, int(kMvLdsBytes));
     if (attr != hipSuccess) return -4;
-    hipLaunchKernelGGL((linear_stream_kernel<T, RPH, PRO, EPI>), dim3(blocks), dim3(256), lds, stream, a);
+    hipLaunchKernelGGL((linear_stream_kernel<T, RPH, PRO, EPI, NT>), dim3(blocks), dim3(NT), lds, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-template <int T, int RPH, int PRO>
+template <int T, int RPH, int PRO, int NT>
 int launch_st_epi(const MvArgs& a, int epi, uint32_t blocks, size_t lds, hipStream_t stream) {
     switch (epi) {
-        case kEpiStore: return launch_st<T, RPH, PRO, kEpiStore>(a, blocks, lds, stream);
-        case kEpiAccumulate: return launch_st<T, RPH, PRO, kEpiAccumulate>(a, blocks, lds, stream);
+        case kEpiStore: return launch_st<T, RPH, PRO, kEpiStore, NT>(a, blocks, lds, stream);
+        case kEpiAccumulate: return launch_st<T, RPH, PRO, kEpiAccumulate, NT>(a, blocks, lds, stream);
         default:
-            if constexpr (RPH >= 2) return launch_st<T, RPH, PRO, kEpiSiluGate>(a, blocks, lds, stream);
+            if constexpr (RPH >= 2) return launch_st<T, RPH, PRO, kEpiSiluGate, NT>(a, blocks, lds, stream);
             return -2;
     }
 }
 
-// Rows per half-wave: 4 when that still gives >= 512 workgroups, else 2 when >= 256, else 1
-// (the gate/up pair: 4 or 2, two of each matrix). F16/BF16 windows are 16 dwords: at most 2.
+// Workgroup shape: many rows per workgroup (x is staged once per workgroup, and its staging
+// traffic otherwise rivals the weights' for the smaller matrices) while the grid still fills the
+// 256 CUs: 512 threads with 4, 2 or 1 rows per half-wave when that gives 128..256 workgroups,
+// else 256 threads with the most rows per half-wave that still gives >= 256 workgroups (the
+// gate/up pair: at least 2, one of each matrix). F16/BF16 windows are 16 dwords: at most 2.
 template <int T>
 int launch_stream_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t stream) {
-    uint32_t rows = 0;
-    for (uint32_t m = 0; m < n_mats; m++) rows += a.n_out[m];
+    const bool silu = epi == kEpiSiluGate;
     constexpr int kMaxRph = T == kF16 || T == kBF16 ? 2 : 4;
-    int rph = rows / 32 >= 512 ? 4 : rows / 16 >= 256 ? 2 : 1;
-    if (rph > kMaxRph) rph = kMaxRph;
-    if (epi == kEpiSiluGate && rph < 2) rph = 2;
-    const int rpm = epi == kEpiSiluGate ? rph / 2 : rph;
-    uint32_t blocks = 0;
-    for (uint32_t m = 0; m < 3; m++) {
-        if (m < n_mats) blocks += (a.n_out[m] + 8 * rpm - 1) / (8 * rpm);
-        a.blk_end[m] = blocks;
+    const int min_rph = silu ? 2 : 1;
+    auto count = [&](int nt, int rph, bool set) {
+        const uint32_t rpw = uint32_t(nt / 32) * uint32_t(silu ? rph / 2 : rph);  // rows per workgroup
+        uint32_t blocks = 0;
+        for (uint32_t m = 0; m < 3; m++) {
+            if (m < n_mats && !(silu && m > 0)) blocks += (a.n_out[m] + rpw - 1) / rpw;
+            if (set) a.blk_end[m] = blocks;
+        }
+        return blocks;
+    };
+    // (measured: a CU holds one 512-thread workgroup of this kernel at a time, so those are
+    // used only when one round of at most 256 of them covers the rows)
+    int nt = 0, rph = min_rph;
+    for (int r = kMaxRph; r >= min_rph && !nt; r /= 2) {
+        const uint32_t b = count(512, r, false);
+        if (b >= 128 && b <= 256) { nt = 512; rph = r; }
     }
-    if (epi == kEpiSiluGate) blocks = a.blk_end[0];
+    for (int r = kMaxRph; r >= min_rph && !nt; r /= 2)
+        if (count(256, r, false) >= 256 || r == min_rph) { nt = 256; rph = r; }
+    const uint32_t blocks = count(nt, rph, true);
     const size_t lds = size_t(a.n_in) * 4 * (pro == kProRmsNorm ? 2 : 1) + 16;
     if (lds > kMvLdsBytes) return -2;
-    auto go = [&](auto pro_tag) -> int {
-        constexpr int P = decltype(pro_tag)::value;
+    auto go = [&](auto pro_tag, auto nt_tag) -> int {
+        constexpr int P = decltype(pro_tag)::value, N = decltype(nt_tag)::value;
         switch (rph) {
-            case 4: if constexpr (kMaxRph >= 4) return launch_st_epi<T, 4, P>(a, epi, blocks, lds, stream); return -2;
-            case 2: return launch_st_epi<T, 2, P>(a, epi, blocks, lds, stream);
-            default: return launch_st_epi<T, 1, P>(a, epi, blocks, lds, stream);
+            case 4: if constexpr (kMaxRph >= 4) return launch_st_epi<T, 4, P, N>(a, epi, blocks, lds, stream); return -2;
+            case 2: return launch_st_epi<T, 2, P, N>(a, epi, blocks, lds, stream);
+            default: return launch_st_epi<T, 1, P, N>(a, epi, blocks, lds, stream);
         }
     };
-    return pro == kProRmsNorm ? go(std::integral_constant<int, kProRmsNorm>{})
-                              : go(std::integral_constant<int, kProNone>{});
+    using R = std::integral_constant<int, kProRmsNorm>;
+    using X = std::integral_constant<int, kProNone>;
+    using N5 = std::integral_constant<int, 512>;
+    using N2 = std::integral_constant<int, 256>;
+    if (pro == kProRmsNorm) return nt == 512 ? go(R{}, N5{}) : go(R{}, N2{});
+    return nt == 512 ? go(X{}, N5{}) : go(X{}, N2{});
 }
 
 // Bytes of LDS a matvec workgroup stages (x, norm weights, rows) plus its reduction slots.
