@@ -120,6 +120,21 @@ typedef struct IngotProjDesc {
 int ingot_proj(const void* const* w, const float* x, const float* norm_w, float* const* out,
                const IngotProjDesc* d, void* stream);
 
+/* One decode token's q/k/v step, end to end: ingot_proj with matrices (wq, wk, wv), the
+ * descriptor's prologue and INGOT_PROJ_STORE, followed by ingot_rope_kv_store for that token
+ * (r->n_tok == 1): q rotated in place, K rotated and V rounded to f16 into the cache rows at
+ * r->dst_offset. For Q4_0, Q4_1, Q8_0, F16 and BF16 weights this is one launch and k, v are not
+ * written; for the other types it is the two launches through k and v. Either way q and the
+ * cache rows equal those of the two calls in sequence, bit for bit. Replaces, for one token,
+ * the encode_rmsnorm + q/k/v encode_linear + rope + rope_k_to_cache + to_half sequence of
+ * src/metal_backend.mm:433-444 (CpuBackend: src/cpu_backend.cpp:36-49).
+ *   q, k, v   f32 [n_head*head_dim], [n_head_kv*head_dim] x2, 16-byte aligned (k, v scratch)
+ *   p         n_mats 3, n_out = {n_head*head_dim, n_head_kv*head_dim, n_head_kv*head_dim}
+ *   r         as for ingot_rope_kv_store (q_stride / kv_stride ignored: rows are dense) */
+int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w, float* q, float* k,
+                       float* v, uint16_t* k_cache, uint16_t* v_cache, const float* inv_freq,
+                       const IngotProjDesc* p, const IngotRopeKvDesc* r, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -78,6 +78,25 @@ int check_linear(const IngotLinearDesc* d) {
     return INGOT_ATTN_OK;
 }
 
+// The descriptor and input checks shared by ingot_proj and ingot_proj_rope_kv.
+int check_proj(const void* const* w, const float* x, const float* norm_w, const IngotProjDesc* d) {
+    if (!d || !w || !x || d->n_in == 0 || d->n_mats < 1 || d->n_mats > 3) return INGOT_ATTN_EINVAL;
+    if (d->prologue > INGOT_PROJ_RMSNORM || d->epilogue > INGOT_PROJ_SILU_GATE) return INGOT_ATTN_EINVAL;
+    uint32_t elems, bytes;
+    linear_block(d->type, elems, bytes);
+    if (elems == 0) return INGOT_ATTN_EUNSUPPORTED;
+    if (d->n_in % 32 != 0 || d->n_in % elems != 0) return INGOT_ATTN_EUNSUPPORTED;
+    if (!aligned16(x)) return INGOT_ATTN_EINVAL;
+    if (d->prologue == INGOT_PROJ_RMSNORM && (!norm_w || !aligned16(norm_w) || !(d->eps >= 0.f)))
+        return INGOT_ATTN_EINVAL;
+    if (d->epilogue == INGOT_PROJ_SILU_GATE && (d->n_mats != 2 || d->n_out[0] != d->n_out[1]))
+        return INGOT_ATTN_EINVAL;
+    for (uint32_t m = 0; m < d->n_mats; m++)
+        if (!w[m] || !aligned16(w[m]) || d->n_out[m] == 0) return INGOT_ATTN_EINVAL;
+    if (uint64_t(d->n_in) / elems * bytes > 0x7fffffffull) return INGOT_ATTN_EUNSUPPORTED;
+    return INGOT_ATTN_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -117,26 +136,48 @@ int ingot_linear(const void* w, const float* x, float* out, void* workspace, siz
 
 int ingot_proj(const void* const* w, const float* x, const float* norm_w, float* const* out,
                const IngotProjDesc* d, void* stream) {
-    if (!d || !w || !x || !out || d->n_in == 0 || d->n_mats < 1 || d->n_mats > 3) return INGOT_ATTN_EINVAL;
-    if (d->prologue > INGOT_PROJ_RMSNORM || d->epilogue > INGOT_PROJ_SILU_GATE) return INGOT_ATTN_EINVAL;
-    uint32_t elems, bytes;
-    linear_block(d->type, elems, bytes);
-    if (elems == 0) return INGOT_ATTN_EUNSUPPORTED;
-    if (d->n_in % 32 != 0 || d->n_in % elems != 0) return INGOT_ATTN_EUNSUPPORTED;
-    if (!aligned16(x)) return INGOT_ATTN_EINVAL;
-    if (d->prologue == INGOT_PROJ_RMSNORM && (!norm_w || !aligned16(norm_w) || !(d->eps >= 0.f)))
-        return INGOT_ATTN_EINVAL;
+    const int rc = check_proj(w, x, norm_w, d);
+    if (rc) return rc;
     const uint32_t n_outs = d->epilogue == INGOT_PROJ_SILU_GATE ? 1 : d->n_mats;
-    if (d->epilogue == INGOT_PROJ_SILU_GATE && (d->n_mats != 2 || d->n_out[0] != d->n_out[1]))
-        return INGOT_ATTN_EINVAL;
-    for (uint32_t m = 0; m < d->n_mats; m++)
-        if (!w[m] || !aligned16(w[m]) || d->n_out[m] == 0) return INGOT_ATTN_EINVAL;
-    if (uint64_t(d->n_in) / elems * bytes > 0x7fffffffull) return INGOT_ATTN_EUNSUPPORTED;
+    if (!out) return INGOT_ATTN_EINVAL;
     for (uint32_t m = 0; m < n_outs; m++)
         if (!out[m] || (reinterpret_cast<uintptr_t>(out[m]) & 3u) != 0) return INGOT_ATTN_EINVAL;
     const int lrc = ingot::launch_proj(d->type, w, x, norm_w, out, d->n_in, d->n_out, d->n_mats,
                                        int(d->prologue), int(d->epilogue), d->eps,
                                        static_cast<hipStream_t>(stream));
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+}
+
+int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w, float* q, float* k,
+                       float* v, uint16_t* k_cache, uint16_t* v_cache, const float* inv_freq,
+                       const IngotProjDesc* p, const IngotRopeKvDesc* r, void* stream) {
+    const int rc = check_proj(w, x, norm_w, p);
+    if (rc) return rc;
+    if (!r || p->n_mats != 3 || p->epilogue != INGOT_PROJ_STORE || r->n_tok != 1) return INGOT_ATTN_EINVAL;
+    if (r->n_head == 0 || r->n_head_kv == 0 || r->head_dim == 0) return INGOT_ATTN_EINVAL;
+    if (r->head_dim % 4 != 0) return INGOT_ATTN_EUNSUPPORTED;
+    const uint64_t qd = uint64_t(r->n_head) * r->head_dim, kvd = uint64_t(r->n_head_kv) * r->head_dim;
+    if (p->n_out[0] != qd || p->n_out[1] != kvd || p->n_out[2] != kvd) return INGOT_ATTN_EINVAL;
+    if (!q || !k || !v || !k_cache || !v_cache || !inv_freq) return INGOT_ATTN_EINVAL;
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || r->dst_offset % 4 != 0 ||
+        (reinterpret_cast<uintptr_t>(k_cache) & 7u) != 0 || (reinterpret_cast<uintptr_t>(v_cache) & 7u) != 0)
+        return INGOT_ATTN_EINVAL;
+    auto* kc = reinterpret_cast<_Float16*>(k_cache) + r->dst_offset;
+    auto* vc = reinterpret_cast<_Float16*>(v_cache) + r->dst_offset;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    // One launch for the streamed weight types; the others take the two-launch sequence
+    // through k and v (the same results).
+    const ingot::ProjRope rope{inv_freq, kc, vc, r->head_dim, r->pos};
+    float* outs[3] = {q, k, v};
+    int lrc = ingot::launch_proj(p->type, w, x, norm_w, outs, p->n_in, p->n_out, 3, int(p->prologue),
+                                 3 /* rope / KV store */, p->eps, st, &rope);
+    if (lrc == -2) {
+        lrc = ingot::launch_proj(p->type, w, x, norm_w, outs, p->n_in, p->n_out, 3, int(p->prologue),
+                                 INGOT_PROJ_STORE, p->eps, st);
+        if (lrc == 0)
+            lrc = ingot::launch_rope_kv_store(q, k, v, kc, vc, inv_freq, r->n_head, r->n_head_kv,
+                                              r->head_dim, r->pos, 1, uint32_t(qd), uint32_t(kvd), st);
+    }
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
 }
 

@@ -42,6 +42,16 @@ __device__ __forceinline__ float row16_sum(float x) {
     return x;
 }
 
+// One RoPE pair (x0, x1) rotated by (c, s) = (cos, sin) of the angle: the first and second
+// element of the result, with every product rounded on its own (no fused multiply-add), so the
+// separate rope kernel and the fused projection epilogue agree bit for bit.
+__device__ __forceinline__ float rope_even(float x0, float x1, float c, float s) {
+    return __fsub_rn(__fmul_rn(x0, c), __fmul_rn(x1, s));
+}
+__device__ __forceinline__ float rope_odd(float x0, float x1, float c, float s) {
+    return __fadd_rn(__fmul_rn(x0, s), __fmul_rn(x1, c));
+}
+
 __device__ __forceinline__ half8 load_half8(const _Float16* p) {
     return *reinterpret_cast<const half8*>(p);
 }

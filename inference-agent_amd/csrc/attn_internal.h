@@ -45,12 +45,22 @@ constexpr uint32_t kLinearMaxTiles = 256;
 int launch_linear(uint32_t type, const void* W, const float* x, float* out, uint32_t n_in,
                   uint32_t n_out, uint32_t n_tok, uint32_t accumulate, uint32_t n_splits,
                   void* workspace, size_t workspace_bytes, hipStream_t stream);
+// The rope / KV-store epilogue's arguments: the cache rows of the token (K and V, f16), the
+// rotary inverse frequencies, head_dim and the position.
+struct ProjRope {
+    const float* inv_freq;
+    _Float16* k_row;
+    _Float16* v_row;
+    uint32_t head_dim, pos;
+};
+
 // One token through n_mats (1..3) matrices of one type sharing x, with the rmsnorm prologue
-// (pro 1, norm weights aux) and the store / accumulate / silu-gate epilogue (epi 0 / 1 / 2).
+// (pro 1, norm weights aux) and the store / accumulate / silu-gate / rope-KV epilogue
+// (epi 0 / 1 / 2 / 3; 3 takes q, k, v and `rope`, and only the streamed types).
 // Returns 0, -2 (type without a kernel, rows too long to stage) or -4 (launch failed).
 int launch_proj(uint32_t type, const void* const* W, const float* x, const float* aux,
                 float* const* out, uint32_t n_in, const uint32_t* n_out, uint32_t n_mats,
-                int pro, int epi, float eps, hipStream_t stream);
+                int pro, int epi, float eps, hipStream_t stream, const ProjRope* rope = nullptr);
 // Split count for the batched path (requested: 0 = choose); `workspace_bytes` bounds it.
 uint32_t linear_splits(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested,
                        size_t workspace_bytes);

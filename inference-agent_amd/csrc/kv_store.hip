@@ -21,9 +21,11 @@ namespace {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
+// (x0, x1) -> (x0 c - x1 s, x0 s + x1 c), each product rounded separately (no fused
+// multiply-add), as the fused projection epilogue computes it too.
 __device__ __forceinline__ float4v rotate2(float4v x, float c0, float s0, float c1, float s1) {
-    return float4v{x[0] * c0 - x[1] * s0, x[0] * s0 + x[1] * c0, x[2] * c1 - x[3] * s1,
-                   x[2] * s1 + x[3] * c1};
+    return float4v{rope_even(x[0], x[1], c0, s0), rope_odd(x[0], x[1], c0, s0),
+                   rope_even(x[2], x[3], c1, s1), rope_odd(x[2], x[3], c1, s1)};
 }
 
 __global__ __launch_bounds__(256) void rope_kv_store_kernel(

@@ -178,7 +178,10 @@ constexpr int kMvChunks = 8;  // 16-byte staging loads per thread per round (one
 //     matrices (gate, up) over the same rows, out0 = silu(s_gate) * s_up with
 //     silu(g) = g / (1 + exp(-g)), as silu_mul_kernel.
 enum : int { kProNone = 0, kProRmsNorm = 1 };
-enum : int { kEpiStore = 0, kEpiAccumulate = 1, kEpiSiluGate = 2 };
+enum : int { kEpiStore = 0, kEpiAccumulate = 1, kEpiSiluGate = 2, kEpiRopeKv = 3 };
+//   kEpiRopeKv: matrices q, k, v of one decode token: q and k rotated by RoPE (pairs (2i, 2i+1)
+//     of each head, angle pos * inv_freq[i], rotated as rope_kv_store_kernel does), q stored in
+//     f32, K and V rounded to f16 into their cache rows (ingot_rope_kv_store's work).
 
 // Up to three matrices of one type sharing n_in and x (q/k/v, gate/up), launched as one grid:
 // blocks [blk_end[m-1], blk_end[m]) take matrix m's rows, R per block.
@@ -191,6 +194,10 @@ struct MvArgs {
     const float* aux;  // rmsnorm weights [n_in]
     uint32_t n_in, row_bytes;
     float eps;
+    // kEpiRopeKv
+    const float* inv_freq;
+    _Float16* cache[2];  // K and V rows of the token
+    uint32_t head_dim, pos;
 };
 
 // R weight rows per matrix per workgroup of 4 waves (2R for the gate/up pair); each wave takes a
@@ -653,16 +660,44 @@ __global__ __launch_bounds__(NT) void linear_stream_kernel(const MvArgs a) {
         float t = row16_sum(acc[i]);
         tot[i] = t + __shfl_xor(t, 16);
     }
+    if constexpr (EPI == kEpiRopeKv) {
+        // RPM is even and row0 + hw * RPM is even: each rotary pair is in one half-wave
+        static_assert(RPM % 2 == 0, "rotary pairs stay in one half-wave");
+        if (l32 < uint32_t(RPM)) {
+            const uint32_t r = row0 + hw * RPM + l32;
+            float val = tot[0];
 #pragma unroll
-    for (int i = 0; i < RPM; i++) {
-        const uint32_t r = row0 + hw * RPM + i;
-        if (l32 == uint32_t(i) && r < n_out) {
-            float* o = a.out[m] + r;
-            if constexpr (EPI == kEpiSiluGate) {
-                const float g = tot[i], u = tot[RPM + i];
-                *o = g / (1.0f + expf(-g)) * u;
-            } else {
-                *o = EPI == kEpiAccumulate ? *o + tot[i] : tot[i];
+            for (int i = 1; i < RPM; i++) val = l32 == uint32_t(i) ? tot[i] : val;
+            if (m < 2) {
+                // partner of the pair
+                float x0 = tot[0], x1 = tot[1];
+#pragma unroll
+                for (int i = 2; i < RPM; i += 2) {
+                    x0 = (l32 >> 1) == uint32_t(i / 2) ? tot[i] : x0;
+                    x1 = (l32 >> 1) == uint32_t(i / 2) ? tot[i + 1] : x1;
+                }
+                const uint32_t pair = (r % a.head_dim) / 2;
+                float sn, cs;
+                sincosf(float(a.pos) * a.inv_freq[pair], &sn, &cs);
+                val = (l32 & 1) ? rope_odd(x0, x1, cs, sn) : rope_even(x0, x1, cs, sn);
+            }
+            if (r < n_out) {
+                if (m == 0) a.out[0][r] = val;
+                else a.cache[m - 1][r] = _Float16(val);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RPM; i++) {
+            const uint32_t r = row0 + hw * RPM + i;
+            if (l32 == uint32_t(i) && r < n_out) {
+                float* o = a.out[m] + r;
+                if constexpr (EPI == kEpiSiluGate) {
+                    const float g = tot[i], u = tot[RPM + i];
+                    *o = g / (1.0f + expf(-g)) * u;
+                } else {
+                    *o = EPI == kEpiAccumulate ? *o + tot[i] : tot[i];
+                }
             }
         }
     }
@@ -683,6 +718,9 @@ int launch_st_epi(const MvArgs& a, int epi, uint32_t blocks, size_t lds, hipStre
     switch (epi) {
         case kEpiStore: return launch_st<T, RPH, PRO, kEpiStore, NT>(a, blocks, lds, stream);
         case kEpiAccumulate: return launch_st<T, RPH, PRO, kEpiAccumulate, NT>(a, blocks, lds, stream);
+        case kEpiRopeKv:
+            if constexpr (RPH >= 2) return launch_st<T, RPH, PRO, kEpiRopeKv, NT>(a, blocks, lds, stream);
+            return -2;
         default:
             if constexpr (RPH >= 2) return launch_st<T, RPH, PRO, kEpiSiluGate, NT>(a, blocks, lds, stream);
             return -2;
@@ -698,7 +736,7 @@ template <int T>
 int launch_stream_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t stream) {
     const bool silu = epi == kEpiSiluGate;
     constexpr int kMaxRph = T == kF16 || T == kBF16 ? 2 : 4;
-    const int min_rph = silu ? 2 : 1;
+    const int min_rph = silu || epi == kEpiRopeKv ? 2 : 1;
     auto count = [&](int nt, int rph, bool set) {
         const uint32_t rpw = uint32_t(nt / 32) * uint32_t(silu ? rph / 2 : rph);  // rows per workgroup
         uint32_t blocks = 0;
@@ -1245,12 +1283,21 @@ size_t linear_workspace_size(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint
 
 int launch_proj(uint32_t type, const void* const* W, const float* x, const float* aux,
                 float* const* out, uint32_t n_in, const uint32_t* n_out, uint32_t n_mats,
-                int pro, int epi, float eps, hipStream_t stream) {
+                int pro, int epi, float eps, hipStream_t stream, const ProjRope* rope) {
     MvArgs a{};
+    if (epi == kEpiRopeKv) {
+        if (!rope || n_mats != 3) return -2;
+        if (!(type == kQ4_0 || type == kQ4_1 || type == kQ8_0 || type == kF16 || type == kBF16)) return -2;
+        a.inv_freq = rope->inv_freq;
+        a.cache[0] = rope->k_row;
+        a.cache[1] = rope->v_row;
+        a.head_dim = rope->head_dim;
+        a.pos = rope->pos;
+    }
     for (uint32_t m = 0; m < n_mats; m++) {
         a.W[m] = static_cast<const uint8_t*>(W[m]);
         a.n_out[m] = n_out[m];
-        a.out[m] = epi == kEpiSiluGate ? out[0] : out[m];
+        a.out[m] = epi == kEpiSiluGate || epi == kEpiRopeKv ? out[0] : out[m];
     }
     a.x = x;
     a.aux = aux;

@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "ingot_attn.h"
+#include "ingot_linear.h"
 
 namespace ingot {
 
@@ -85,6 +86,21 @@ public:
                                    static_cast<uint16_t*>(vcache_), static_cast<float*>(inv_freq_),
                                    &d, stream_),
                "kv store");
+    }
+
+    // One decode token's q/k/v step in one call (ingot_proj_rope_kv): the projections of x
+    // (after the rmsnorm when p.prologue asks for it) by w = {wq, wk, wv}, RoPE, and K/V into
+    // the cache rows of (layer, pos); q receives the rotated queries, k and v are scratch.
+    void proj_kv_store(int layer, int pos, const void* const* w, const float* x, const float* norm_w,
+                       const IngotProjDesc& p, float* q, float* k, float* v) {
+        check_range(layer, pos, 1);
+        IngotRopeKvDesc d{uint32_t(c_.n_head), uint32_t(c_.n_head_kv), uint32_t(c_.head_dim),
+                          uint32_t(pos), 1u, slot(layer, pos), uint32_t(c_.n_head * c_.head_dim),
+                          uint32_t(kv_dim_)};
+        status(ingot_proj_rope_kv(w, x, norm_w, q, k, v, static_cast<uint16_t*>(kcache_),
+                                  static_cast<uint16_t*>(vcache_), static_cast<float*>(inv_freq_), &p, &d,
+                                  stream_),
+               "rmsnorm+qkv+kv store");
     }
 
     // encode_attention: out [n_tok][n_head*head_dim] = causal attention of q (rotated) over the

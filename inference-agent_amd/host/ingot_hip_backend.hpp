@@ -10,8 +10,9 @@
 //   embedding rows; per layer: rmsnorm, q/k/v projections, rope(q) + KV store, attention,
 //   x += wo·attn, rmsnorm, gate/up projections, silu(gate)*up, x += down·gate;
 //   rmsnorm of the last token and the logits projection.
-// For one token (decode) rmsnorm + q/k/v, rmsnorm + gate/up + silu and rmsnorm + logits are one
-// ingot_proj launch each (the same results as the separate calls, bit for bit).
+// For one token (decode) rmsnorm + q/k/v + RoPE + KV store (ingot_proj_rope_kv), rmsnorm +
+// gate/up + silu and rmsnorm + logits (ingot_proj) are one launch each (the same results as the
+// separate calls, bit for bit).
 // The model arrives as HostModel, the reference's Model/Layer/Config (src/model.h:8-28) with each
 // gguf::TensorInfo reduced to what the kernels read (type, ne, bytes in the GGUF layout); the
 // weights are copied to the device as they are (no dequantization, no repacking).
@@ -133,18 +134,28 @@ public:
             "embedding");
         for (int l = 0; l < m_.n_layer; l++) {
             const DevLayer& L = layers_[size_t(l)];
-            // One token: rmsnorm + q/k/v in one launch (ingot_proj) when the three share a type.
+            // One token: rmsnorm + q/k/v + RoPE + KV store in one call (ingot_proj_rope_kv) when
+            // the three matrices share a type.
             if (n == 1 && L.wq.type == L.wk.type && L.wq.type == L.wv.type) {
-                const Dev* w[3] = {&L.wq, &L.wk, &L.wv};
-                float* outs[3] = {q_, k_, v_};
-                proj(w, 3, x_, L.attn_norm, outs, INGOT_PROJ_RMSNORM, INGOT_PROJ_STORE, "rmsnorm+qkv");
+                IngotProjDesc d{};
+                d.type = L.wq.type;
+                d.n_in = ne;
+                d.n_mats = 3;
+                d.n_out[0] = qd;
+                d.n_out[1] = kvd;
+                d.n_out[2] = kvd;
+                d.prologue = INGOT_PROJ_RMSNORM;
+                d.epilogue = INGOT_PROJ_STORE;
+                d.eps = m_.rms_eps;
+                const void* w[3] = {L.wq.ptr, L.wk.ptr, L.wv.ptr};
+                attn_->proj_kv_store(l, pos, w, x_, L.attn_norm, d, q_, k_, v_);
             } else {
                 abi(ingot_rmsnorm(x_, L.attn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
                 linear(L.wq, h_, q_, ne, qd, un, false);
                 linear(L.wk, h_, k_, ne, kvd, un, false);
                 linear(L.wv, h_, v_, ne, kvd, un, false);
+                attn_->kv_store(l, pos, n, q_, k_, v_);
             }
-            attn_->kv_store(l, pos, n, q_, k_, v_);
             attn_->attention(l, pos, n, q_, attn_out_);
             linear(L.wo, attn_out_, x_, qd, ne, un, true);
             // One token: rmsnorm + gate/up + silu(gate)*up in one launch.

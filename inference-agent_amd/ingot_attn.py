@@ -33,6 +33,7 @@ EXPORTS = (
     "ingot_linear_workspace_size",
     "ingot_linear",
     "ingot_proj",
+    "ingot_proj_rope_kv",
     "ingot_rmsnorm",
     "ingot_silu_mul",
     "ingot_get_rows",
@@ -163,6 +164,9 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ingot_proj.argtypes = [ctypes.POINTER(c_void_p), c_void_p, c_void_p, ctypes.POINTER(c_void_p),
                                ctypes.POINTER(ProjDesc), c_void_p]
     lib.ingot_proj.restype = c_int
+    lib.ingot_proj_rope_kv.argtypes = [ctypes.POINTER(c_void_p), c_void_p, c_void_p] + [c_void_p] * 6 + [
+        ctypes.POINTER(ProjDesc), ctypes.POINTER(RopeKvDesc), c_void_p]
+    lib.ingot_proj_rope_kv.restype = c_int
     lib.ingot_rmsnorm.argtypes = [c_void_p, c_void_p, c_void_p, c_uint32, c_uint32, c_float, c_void_p]
     lib.ingot_rmsnorm.restype = c_int
     lib.ingot_silu_mul.argtypes = [c_void_p, c_void_p, c_uint64, c_void_p]
@@ -355,6 +359,20 @@ def proj(ws, x, outs, desc: ProjDesc, norm_w=None, stream=None):
                                    ctypes.byref(desc), _stream_ptr(stream))
     _check(rc, "ingot_proj")
     return outs
+
+
+def proj_rope_kv(ws, x, q, k, v, k_cache, v_cache, inv_freq, desc: ProjDesc, rope: "RopeKvDesc",
+                 norm_w=None, stream=None):
+    """One decode token: (rmsnorm +) q/k/v projections, RoPE on q and k, K/V into the cache rows
+    (ingot_proj_rope_kv; k and v are scratch)."""
+    wp = (c_void_p * 3)(*[w.data_ptr() for w in ws])
+    rc = load_library().ingot_proj_rope_kv(
+        wp, c_void_p(x.data_ptr()), c_void_p(norm_w.data_ptr() if norm_w is not None else 0),
+        c_void_p(q.data_ptr()), c_void_p(k.data_ptr()), c_void_p(v.data_ptr()),
+        c_void_p(k_cache.data_ptr()), c_void_p(v_cache.data_ptr()), c_void_p(inv_freq.data_ptr()),
+        ctypes.byref(desc), ctypes.byref(rope), _stream_ptr(stream))
+    _check(rc, "ingot_proj_rope_kv")
+    return q
 
 
 def rmsnorm(x, w, out, n, n_rows, eps, stream=None):

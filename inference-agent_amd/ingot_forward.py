@@ -4,9 +4,10 @@ class `ingot::HipBackend` (host/ingot_hip_backend.hpp), used by the tests and th
 Follows `MetalBackend::forward_batch` (src/metal_backend.mm:419-471) step by step: embedding
 rows; per layer rmsnorm, q/k/v projections, RoPE + KV-cache store, attention, wo with the
 residual add, rmsnorm, gate/up projections, silu_mul, down with the residual add; the final
-rmsnorm of the last token and the logits projection. For one token (decode) the rmsnorm and
-the q/k/v projections are one `ingot_proj` launch, as are rmsnorm + gate/up + silu_mul and the
-final rmsnorm + logits (identical results, fewer launches). Every step is one libingot_attn.so
+rmsnorm of the last token and the logits projection. For one token (decode) the rmsnorm, the
+q/k/v projections, RoPE and the KV store are one `ingot_proj_rope_kv` call, rmsnorm + gate/up +
+silu_mul and the final rmsnorm + logits one `ingot_proj` launch each (identical results, fewer
+launches). Every step is one libingot_attn.so
 call;
 PyTorch only holds device memory and the stream. Errors are the reference's
 (src/metal_backend.mm:421-424): "… batch size out of range", "context window exceeded",
@@ -90,19 +91,19 @@ class HipForward:
         ia.get_rows(E[0], E[1], ne, c["n_vocab"], tok, n, self.x)
         eps = c["rms_eps"]
         for l, L in enumerate(self.layers):
-            qkv_fused = n == 1 and L["wq"][0] == L["wk"][0] == L["wv"][0]
-            if qkv_fused:
-                ia.proj([L["wq"][1], L["wk"][1], L["wv"][1]], self.x, [self.q, self.k, self.v],
-                        ia.proj_desc(L["wq"][0], ne, [qd, kvd, kvd], prologue=ia.PROJ_RMSNORM, eps=eps),
-                        norm_w=L["attn_norm"])
+            rope = ia.rope_kv_desc(c["n_head"], c["n_head_kv"], c["head_dim"], pos, n,
+                                   dst_offset=(l * self.n_ctx + pos) * kvd)
+            if n == 1 and L["wq"][0] == L["wk"][0] == L["wv"][0]:
+                ia.proj_rope_kv([L["wq"][1], L["wk"][1], L["wv"][1]], self.x, self.q, self.k, self.v,
+                                self.k_cache, self.v_cache, self.inv_freq,
+                                ia.proj_desc(L["wq"][0], ne, [qd, kvd, kvd], prologue=ia.PROJ_RMSNORM, eps=eps),
+                                rope, norm_w=L["attn_norm"])
             else:
                 ia.rmsnorm(self.x, L["attn_norm"], self.h, ne, n, eps)
                 self._lin(L["wq"], self.h, self.q, ne, qd, n)
                 self._lin(L["wk"], self.h, self.k, ne, kvd, n)
                 self._lin(L["wv"], self.h, self.v, ne, kvd, n)
-            ia.rope_kv_store(self.q, self.k, self.v, self.k_cache, self.v_cache, self.inv_freq,
-                             ia.rope_kv_desc(c["n_head"], c["n_head_kv"], c["head_dim"], pos, n,
-                                             dst_offset=(l * self.n_ctx + pos) * kvd))
+                ia.rope_kv_store(self.q, self.k, self.v, self.k_cache, self.v_cache, self.inv_freq, rope)
             kv_offset = l * self.n_ctx * kvd
             if n == 1:
                 ia.attn_decode(self.q, self.k_cache, self.v_cache, self.attn,

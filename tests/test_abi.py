@@ -217,3 +217,28 @@ def test_proj_descriptor_checks(lib):
     assert call(ia.proj_desc("F16", 256, [4], epilogue=2)) == -1
     assert call(ia.proj_desc("F16", 256, [4, 8], epilogue=2)) == -1
     assert call(ia.proj_desc("F16", 256, [4, 4, 4], epilogue=2)) == -1
+
+
+def test_proj_rope_kv_checks(lib):
+    """Argument checks of the fused q/k/v + RoPE + KV-store call (all rejected before a launch)."""
+    import ingot_attn as ia
+
+    P = ctypes.c_void_p
+    a = P(1 << 20)
+    w = (ctypes.c_void_p * 3)(a, a, a)
+    good_p = ia.proj_desc("Q4_0", 3072, [3072, 1024, 1024], prologue=ia.PROJ_RMSNORM, eps=1e-5)
+    good_r = ia.rope_kv_desc(24, 8, 128, 5, 1, dst_offset=5 * 1024)
+
+    def call(p=good_p, r=good_r, q=a, kc=a, inv=a):
+        return lib.ingot_proj_rope_kv(w, a, a, q, a, a, kc, a, inv, ctypes.byref(p) if p is not None else None,
+                                      ctypes.byref(r) if r is not None else None, None)
+
+    assert call(p=None) == -1 and call(r=None) == -1
+    assert call(p=ia.proj_desc("Q4_0", 3072, [3072, 1024])) == -1             # three matrices
+    assert call(p=ia.proj_desc("Q4_0", 3072, [3072, 1024, 1024], epilogue=1)) == -1
+    assert call(p=ia.proj_desc("Q4_0", 3072, [3072, 1024, 512])) == -1        # v rows != kv dim
+    assert call(r=ia.rope_kv_desc(24, 8, 128, 5, 2)) == -1                      # one token only
+    assert call(r=ia.rope_kv_desc(24, 8, 130, 5, 1)) in (-1, -2)                # head_dim % 4
+    assert call(q=None) == -1 and call(kc=None) == -1 and call(inv=None) == -1
+    assert call(q=P((1 << 20) + 4)) == -1                                       # q alignment
+    assert call(r=ia.rope_kv_desc(24, 8, 128, 5, 1, dst_offset=2)) == -1      # cache row alignment

@@ -152,3 +152,39 @@ def test_rows_too_long(dev):
     out = torch.zeros(4, device=dev)
     with pytest.raises(RuntimeError):
         ia.proj([w], x, [out], ia.proj_desc("Q4_0", n_in, [4], prologue=ia.PROJ_RMSNORM, eps=EPS), norm_w=x)
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("pos", [0, 1, 777, 4095])
+def test_proj_rope_kv(dev, t, pos):
+    """rmsnorm + q/k/v + RoPE + KV store in one call equals ingot_proj (store) followed by
+    ingot_rope_kv_store, bit for bit: q, the written K/V cache rows, and every other cache row
+    keeps its canary bits."""
+    import torch
+    import ingot_attn as ia
+
+    n_head, n_head_kv, hd, n_in, n_ctx = 24, 8, 128, 3072, 4096 + 8
+    qd, kvd = n_head * hd, n_head_kv * hd
+    x, nw, raws = _inputs(t, n_in, (qd, kvd, kvd), seed=11 + pos)
+    wd = [_t(r.reshape(-1), dev) for r in raws]
+    inv = torch.tensor([500000.0 ** (-2 * i / hd) for i in range(hd // 2)], dtype=torch.float32, device=dev)
+    canary = torch.full((n_ctx, kvd), 0x7E00, dtype=torch.int16, device=dev).view(torch.float16)
+    desc = ia.proj_desc(t, n_in, [qd, kvd, kvd], prologue=ia.PROJ_RMSNORM, eps=EPS)
+    rope = ia.rope_kv_desc(n_head, n_head_kv, hd, pos, 1, dst_offset=pos * kvd)
+    # fused
+    q1, k1, v1 = (torch.zeros(n, device=dev) for n in (qd, kvd, kvd))
+    kc1, vc1 = canary.clone(), canary.clone()
+    ia.proj_rope_kv(wd, _t(x, dev), q1, k1, v1, kc1, vc1, inv, desc, rope, norm_w=_t(nw, dev))
+    # two calls
+    q2, k2, v2 = (torch.zeros(n, device=dev) for n in (qd, kvd, kvd))
+    kc2, vc2 = canary.clone(), canary.clone()
+    ia.proj(wd, _t(x, dev), [q2, k2, v2], desc, norm_w=_t(nw, dev))
+    ia.rope_kv_store(q2, k2, v2, kc2, vc2, inv, rope)
+    torch.cuda.synchronize()
+    assert torch.equal(q1, q2), f"{t} pos {pos}: q differs"
+    assert torch.equal(kc1.view(torch.int16), kc2.view(torch.int16)), f"{t} pos {pos}: K cache differs"
+    assert torch.equal(vc1.view(torch.int16), vc2.view(torch.int16)), f"{t} pos {pos}: V cache differs"
+    untouched = torch.ones(n_ctx, dtype=torch.bool, device=dev)
+    untouched[pos] = False
+    assert bool((kc1.view(torch.int16)[untouched] == 0x7E00).all())
+    assert bool((vc1.view(torch.int16)[untouched] == 0x7E00).all())
