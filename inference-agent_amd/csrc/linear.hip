@@ -891,6 +891,42 @@ __device__ __forceinline__ void load_raw(Raw<T>& r, const uint8_t* row, uint32_t
 }
 
 // The f16 B fragment of step half s.
+// load_raw from a row staged in LDS. A quantized block is only 2-byte aligned, so the 8 or 16
+// quant bytes are read as dword-aligned dwords and realigned with v_alignbyte (an 8-byte LDS
+// read at a 2-byte aligned address stalls on the unaligned access).
+// 8 bytes at a 2-byte aligned LDS address, as two dwords.
+__device__ __forceinline__ void lds_8bytes(const uint8_t* a, uint32_t& lo, uint32_t& hi) {
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(a)) & 3;
+    const uint32_t* p = reinterpret_cast<const uint32_t*>(a - sh);
+    const uint32_t w0 = p[0], w1 = p[1], w2 = p[2];
+    lo = __builtin_amdgcn_alignbyte(w1, w0, sh);
+    hi = __builtin_amdgcn_alignbyte(w2, w1, sh);
+}
+
+template <int T>
+__device__ __forceinline__ void load_raw_lds(Raw<T>& r, const uint8_t* row, uint32_t k0, uint32_t h) {
+    if constexpr (T == kQ4_0) {
+        const uint8_t* b = row + 18 * (k0 / 32);
+        r.d = ld_u16(b);
+        lds_8bytes(b + 2 + 8 * h, r.q[0], r.q[1]);
+    } else if constexpr (T == kQ8_0) {
+        const uint8_t* b = row + 34 * (k0 / 32);
+        r.d = ld_u16(b);
+        for (int s = 0; s < 2; s++) lds_8bytes(b + 2 + 16 * s + 8 * h, r.q[s][0], r.q[s][1]);
+    } else {
+        load_raw<T>(r, row, k0, h);
+    }
+}
+
+// Block types whose B fragments hold their 8 k values in the order 0,2,1,3,4,6,5,7: two
+// elements two bytes apart share a 32-bit word, so one masked word gives a packed half pair.
+template <int T>
+constexpr bool kFragSwap13 = T == kQ4_0 || T == kQ8_0;
+
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    return (a & m) | c;  // v_and_or_b32
+}
+
 template <int T>
 __device__ __forceinline__ half8 frag(const Raw<T>& r, int s, uint32_t k0) {
     half8 o;
@@ -907,22 +943,37 @@ __device__ __forceinline__ half8 frag(const Raw<T>& r, int s, uint32_t k0) {
             o[2 * i + 1] = _Float16(__uint_as_float(r.v[s][i] & 0xFFFF0000u));
         }
     } else if constexpr (T == kQ8_0) {
-        const float d = f16_bits(r.d);
-        for (int i = 0; i < 8; i++) o[i] = _Float16(d * float(int8_t(byte_of(r.q[s][0], r.q[s][1], i))));
+        // Packed f16, k order 0,2,1,3 per word: the byte q ^ 0x80 = q + 128 becomes the half
+        // 1024 + q + 128 (exact), minus 1152 gives q, times d rounds once — d*q rounded to half,
+        // as when formed in f32.
+        typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+        const _Float16 dh = __builtin_bit_cast(_Float16, uint16_t(r.d));
+        const h2 dd = {dh, dh}, off = {_Float16(-1152.f), _Float16(-1152.f)};
+        for (int w = 0; w < 2; w++) {
+            const uint32_t q = r.q[s][w] ^ 0x80808080u;
+            const h2 a = (__builtin_bit_cast(h2, and_or(q, 0x00FF00FFu, 0x64006400u)) + off) * dd;
+            const h2 b = (__builtin_bit_cast(h2, and_or(q >> 8, 0x00FF00FFu, 0x64006400u)) + off) * dd;
+            o[4 * w] = a[0];      // k 4w
+            o[4 * w + 1] = a[1];  // k 4w + 2
+            o[4 * w + 2] = b[0];  // k 4w + 1
+            o[4 * w + 3] = b[1];  // k 4w + 3
+        }
     } else if constexpr (T == kQ4_0) {
-        // Packed f16: the nibble n becomes the half 1024 + n (bits 0x6400 | n), minus 1032 gives
-        // n - 8 exactly, times d rounds once — the same value as d*(n-8) formed in f32 and
-        // rounded to half.
+        // Packed f16, k order 0,2,1,3 per word: the nibble n becomes the half 1024 + n (bits
+        // 0x6400 | n), minus 1032 gives n - 8 exactly, times d rounds once — the same value as
+        // d*(n-8) formed in f32 and rounded to half.
         typedef _Float16 h2 __attribute__((ext_vector_type(2)));
         const _Float16 dh = __builtin_bit_cast(_Float16, uint16_t(r.d));
         const h2 dd = {dh, dh}, off = {_Float16(-1032.f), _Float16(-1032.f)};
         const uint32_t sh = 4 * s;  // elements 16..31 of the block are the high nibbles
-        for (int p = 0; p < 4; p++) {
-            // bytes 2p, 2p+1 into the low byte of each half
-            const uint32_t v = __builtin_amdgcn_perm(0u, p < 2 ? r.q[0] : r.q[1], (p & 1) ? 0x0c030c02u : 0x0c010c00u);
-            const h2 hv = (__builtin_bit_cast(h2, ((v >> sh) & 0x000F000Fu) | 0x64006400u) + off) * dd;
-            o[2 * p] = hv[0];
-            o[2 * p + 1] = hv[1];
+        for (int w = 0; w < 2; w++) {
+            const uint32_t q = r.q[w] >> sh;
+            const h2 a = (__builtin_bit_cast(h2, and_or(q, 0x000F000Fu, 0x64006400u)) + off) * dd;
+            const h2 b = (__builtin_bit_cast(h2, and_or(q >> 8, 0x000F000Fu, 0x64006400u)) + off) * dd;
+            o[4 * w] = a[0];      // k 4w
+            o[4 * w + 1] = a[1];  // k 4w + 2
+            o[4 * w + 2] = b[0];  // k 4w + 1
+            o[4 * w + 3] = b[1];  // k 4w + 3
         }
     } else if constexpr (T == kQ4_1) {
         const float d = f16_bits(r.d);
@@ -968,7 +1019,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     // Register rings: W raw bytes DW steps ahead, x DX steps ahead of its LDS double buffer.
     // A wait for the x of step t+1 (issued at step t+1-DX, before that step's W load) leaves
     // every later load in flight, so both streams keep DX-1 or more steps of slack.
-    constexpr int DW = 4, DX = 4;
+    constexpr int DW = 8, DX = 8;
     // Ring slots are indexed by the unrolled position d, equal to t mod DX and t mod 2 only
     // when DW is a multiple of both.
     static_assert(DW % DX == 0 && DW % 2 == 0, "ring depths");
@@ -1003,10 +1054,13 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         xr[slot] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
                                                    xrs, int(xoff + 4 * min(t, steps - 1) * kMmK), 0, 0));
     };
+    // (for the block types whose fragments come out in the k order 0,2,1,3 within each group of
+    // four, x is staged in the same order: the MFMA pairs A and B elements by position)
     auto store_x = [&](int slot, int buf) {
         typedef _Float16 half4_ __attribute__((ext_vector_type(4)));
-        const half4_ v = {_Float16(xr[slot][0]), _Float16(xr[slot][1]), _Float16(xr[slot][2]),
-                          _Float16(xr[slot][3])};
+        const half4_ v = kFragSwap13<T>
+            ? half4_{_Float16(xr[slot][0]), _Float16(xr[slot][2]), _Float16(xr[slot][1]), _Float16(xr[slot][3])}
+            : half4_{_Float16(xr[slot][0]), _Float16(xr[slot][1]), _Float16(xr[slot][2]), _Float16(xr[slot][3])};
         *reinterpret_cast<half4_*>(&xs[buf][st_tok * kXPitch + st_k]) = v;
     };
 
@@ -1073,7 +1127,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                     const int buf = d & 1;
                     load_x(d % DX, t + DX);
                     Raw<T> r;
-                    load_raw<T>(r, wrow, u * kMmK, h);
+                    load_raw_lds<T>(r, wrow, u * kMmK, h);
                     half8 b[2];
                     for (int s = 0; s < 2; s++) b[s] = frag<T>(r, s, kbeg + t * kMmK);
 #pragma unroll
