@@ -1023,7 +1023,6 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     // Ring slots are indexed by the unrolled position d, equal to t mod DX and t mod 2 only
     // when DW is a multiple of both.
     static_assert(DW % DX == 0 && DW % 2 == 0, "ring depths");
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][kMmToks * kXPitch];
     const uint32_t tid = threadIdx.x, wave = tid / 64, lane = tid % 64;
     const uint32_t n = lane % 32, h = lane / 32;
 
@@ -1048,36 +1047,30 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const uint32_t x_rows = min(n_tok - tok0, uint32_t(kMmToks));
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(x + size_t(tok0) * n_in), 0, int(4 * x_rows * n_in), kBufferFlags);
-    const uint32_t xoff = 4 * (min(st_tok, x_rows - 1) * n_in + kbeg + st_k);
-    float4v xr[DX];
-    auto load_x = [&](int slot, uint32_t t) {
-        xr[slot] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   xrs, int(xoff + 4 * min(t, steps - 1) * kMmK), 0, 0));
-    };
-    // (for the block types whose fragments come out in the k order 0,2,1,3 within each group of
-    // four, x is staged in the same order: the MFMA pairs A and B elements by position)
-    auto store_x = [&](int slot, int buf) {
-        typedef _Float16 half4_ __attribute__((ext_vector_type(4)));
-        const half4_ v = kFragSwap13<T>
-            ? half4_{_Float16(xr[slot][0]), _Float16(xr[slot][2]), _Float16(xr[slot][1]), _Float16(xr[slot][3])}
-            : half4_{_Float16(xr[slot][0]), _Float16(xr[slot][1]), _Float16(xr[slot][2]), _Float16(xr[slot][3])};
-        *reinterpret_cast<half4_*>(&xs[buf][st_tok * kXPitch + st_k]) = v;
-    };
-
     float16v_ acc[2];
     for (int i = 0; i < 2; i++)
         for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
 
     if constexpr (LW) {
-        // W through LDS: thread t loads 16-byte chunks t, t+512, ... of the stage (row-major,
-        // so 8-10 consecutive lanes cover one row's piece: whole cache lines), two stages ahead
-        // in registers; the chunks of stage j+1 are written to LDS buffer (j+1)&1 at the end of
-        // stage j. Each wave then builds its B operands from its 32 rows in LDS.
+        // W and x through LDS, one stage (`ks` elements of k) at a time, one barrier per stage:
+        // thread t loads 16-byte chunks t, t+512, ... of the W stage (row-major, so 8-10
+        // consecutive lanes cover one row's piece: whole cache lines), two stages ahead in
+        // registers, and x's float4s k = 32i + 4(t%8) of token t/8, one stage ahead; both are
+        // written to the idle LDS buffers at the end of a stage (x as f16). Each wave then
+        // builds its B operands from its 32 rows in LDS and reads its A operands from the x
+        // stage: P steps of 4 MFMAs between barriers.
         constexpr uint32_t KS = Stage<T>::ks, P = KS / kMmK, SB = Stage<T>::bytes;
         constexpr uint32_t PITCH = Stage<T>::pitch, CH = SB / 16;
         constexpr uint32_t NCH = (kMmRows * CH + 511) / 512;
-        constexpr uint32_t JU = P >= DX ? 2 : 2 * DX / P;  // stages per unrolled block
-        static_assert(KS % kMmK == 0 && (JU * P) % DX == 0, "stage shape");
+        // x stages of XK elements (NXS per W stage), as large as the LDS left by the W double
+        // buffer allows
+        constexpr uint32_t XK = T == kQ8_0 ? 64 : (KS < 128 ? KS : 128);
+        constexpr uint32_t NXS = KS / XK, PX = XK / kMmK;  // x stages per W stage, steps per x stage
+        constexpr uint32_t XP = XK + 8;    // halves per token row of an x stage (conflict-free A reads)
+        constexpr uint32_t XF4 = XK / 32;  // float4 x loads per thread per x stage
+        static_assert(KS % XK == 0 && XK % kMmK == 0 && kMmToks * XK == 512 * 4 * XF4, "stage shape");
+        static_assert(2 * kMmRows * PITCH + 2 * kMmToks * XP * 2 <= 160 * 1024, "LDS");
+        __shared__ __attribute__((aligned(16))) _Float16 xst[2][kMmToks * XP];
         extern __shared__ __attribute__((aligned(16))) uint8_t wsm[];  // [2][kMmRows][PITCH]
         const uint32_t nst = steps / P;
         const uint32_t rows_here = min(n_out - rt * kMmRows, uint32_t(kMmRows));
@@ -1104,46 +1097,89 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
             for (uint32_t i = 0; i < NCH; i++)
                 if (tid + 512 * i < kMmRows * CH) *reinterpret_cast<u32x4*>(base + loff[i]) = wr[slot][i];
         };
-
+        const uint32_t xk = 4 * (tid % 8);
+        const uint32_t xso = 4 * (min(st_tok, x_rows - 1) * n_in + kbeg + xk);
+        float4v xq[XF4];
+        const uint32_t nxs = nst * NXS;  // x stages
+        auto load_xs = [&](uint32_t j) {
+            const uint32_t kb = min(j, nxs - 1) * XK;
 #pragma unroll
-        for (int d = 0; d < DX; d++) load_x(d, d);
+            for (uint32_t i = 0; i < XF4; i++)
+                xq[i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                        xrs, int(xso + 4 * (kb + 32 * i)), 0, 0));
+        };
+        auto store_xs = [&](int buf) {
+            typedef _Float16 half4_ __attribute__((ext_vector_type(4)));
+#pragma unroll
+            for (uint32_t i = 0; i < XF4; i++) {
+                const float4v v = xq[i];
+                const half4_ hv = kFragSwap13<T>
+                    ? half4_{_Float16(v[0]), _Float16(v[2]), _Float16(v[1]), _Float16(v[3])}
+                    : half4_{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+                *reinterpret_cast<half4_*>(&xst[buf][st_tok * XP + 32 * i + xk]) = hv;
+            }
+        };
+
+        load_xs(0);
         load_w(0, 0);
         load_w(1, 1);
-        store_x(0, 0);
+        store_xs(0);
         store_w(0);
+        load_xs(1);
         __syncthreads();
 
-        for (uint32_t j0 = 0; j0 < nst; j0 += JU) {
+        for (uint32_t j0 = 0; j0 < nst; j0 += 2) {
 #pragma unroll
-            for (uint32_t jj = 0; jj < JU; jj++) {
+            for (uint32_t jj = 0; jj < 2; jj++) {
                 const uint32_t j = j0 + jj;
                 if (j >= nst) break;
-                const uint8_t* wrow = wsm + (jj & 1) * (kMmRows * PITCH) + (wave * kMmRowsWave + n) * PITCH;
-                load_w(jj & 1, j + 2);  // this slot's stage j is already in LDS
+                const uint8_t* wrow = wsm + jj * (kMmRows * PITCH) + (wave * kMmRowsWave + n) * PITCH;
+                load_w(jj, j + 2);  // this slot's stage j is already in LDS
 #pragma unroll
-                for (uint32_t u = 0; u < P; u++) {
-                    const uint32_t t = j * P + u;
-                    const uint32_t d = jj * P + u;  // == t mod (JU*P): ring slots are compile-time
-                    const int buf = d & 1;
-                    load_x(d % DX, t + DX);
-                    Raw<T> r;
-                    load_raw_lds<T>(r, wrow, u * kMmK, h);
-                    half8 b[2];
-                    for (int s = 0; s < 2; s++) b[s] = frag<T>(r, s, kbeg + t * kMmK);
+                for (uint32_t xs_i = 0; xs_i < NXS; xs_i++) {
+                    const uint32_t xb = (jj * NXS + xs_i) & 1;  // x buffer of x stage j*NXS + xs_i
+                    const _Float16* xsb = &xst[xb][0];
 #pragma unroll
-                    for (int s = 0; s < 2; s++) {
-                        for (int i = 0; i < 2; i++) {
-                            const half8 a = *reinterpret_cast<const half8*>(&xs[buf][(32 * i + n) * kXPitch + 16 * s + 8 * h]);
-                            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[s], acc[i], 0, 0, 0);
+                    for (uint32_t v = 0; v < PX; v++) {
+                        const uint32_t u = xs_i * PX + v;  // step within the W stage
+                        const uint32_t t = j * P + u;
+                        Raw<T> r;
+                        load_raw_lds<T>(r, wrow, u * kMmK, h);
+                        half8 b[2];
+                        for (int s = 0; s < 2; s++) b[s] = frag<T>(r, s, kbeg + t * kMmK);
+#pragma unroll
+                        for (int s = 0; s < 2; s++) {
+                            for (int i = 0; i < 2; i++) {
+                                const half8 a = *reinterpret_cast<const half8*>(&xsb[(32 * i + n) * XP + v * kMmK + 16 * s + 8 * h]);
+                                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[s], acc[i], 0, 0, 0);
+                            }
                         }
                     }
-                    store_x((d + 1) % DX, buf ^ 1);  // x of step t+1
-                    if (u == P - 1) store_w((jj + 1) & 1);  // W of stage j+1
+                    store_xs(xb ^ 1);  // x of the next x stage
+                    if (xs_i == NXS - 1) store_w(jj ^ 1);  // W of stage j+1
+                    load_xs(j * NXS + xs_i + 2);
                     __syncthreads();
                 }
             }
         }
     } else {
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][kMmToks * kXPitch];
+    const uint32_t xoff = 4 * (min(st_tok, x_rows - 1) * n_in + kbeg + st_k);
+    float4v xr[DX];
+    auto load_x = [&](int slot, uint32_t t) {
+        xr[slot] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   xrs, int(xoff + 4 * min(t, steps - 1) * kMmK), 0, 0));
+    };
+    // (for the block types whose fragments come out in the k order 0,2,1,3 within each group of
+    // four, x is staged in the same order: the MFMA pairs A and B elements by position)
+    auto store_x = [&](int slot, int buf) {
+        typedef _Float16 half4_ __attribute__((ext_vector_type(4)));
+        const half4_ v = kFragSwap13<T>
+            ? half4_{_Float16(xr[slot][0]), _Float16(xr[slot][2]), _Float16(xr[slot][1]), _Float16(xr[slot][3])}
+            : half4_{_Float16(xr[slot][0]), _Float16(xr[slot][1]), _Float16(xr[slot][2]), _Float16(xr[slot][3])};
+        *reinterpret_cast<half4_*>(&xs[buf][st_tok * kXPitch + st_k]) = v;
+    };
+
     const uint8_t* row = W + size_t(min(rowbase + n, n_out - 1)) * row_bytes;
     const uint32_t k_last = kbeg + (steps - 1) * kMmK;
 
