@@ -30,6 +30,7 @@ import argparse
 import json
 import os
 import sys
+import statistics
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -68,7 +69,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    help="all | decode | prefill | kvstore | linear | one of "
+                    help="all | decode | prefill | kvstore | linear | model | probes | one of "
                     + ", ".join(list(DECODE) + list(PREFILL) + list(KVSTORE) + list(LINEAR)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -239,23 +240,62 @@ def time_steps(torch, fn, steps, warmup, use_graph):
 
 
 def cpu_baseline(W, seconds):
-    """The CPU oracle (C++ restatement of src/cpu_backend.cpp:51-69) on the host cores."""
+    """The CPU oracle (C++ restatement of src/cpu_backend.cpp:51-69) on the host cores: the
+    median of the per-call times over `seconds` of calls on every thread used, and the median of
+    5 calls on one thread."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle_lib
 
     threads = max(1, min(24, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), os.cpu_count() or 1))
     w = W.C3
     q, kb, vb = W.make_inputs(w)
-    oracle_lib.attn_decode(q, kb, vb, W.N_HEAD, W.N_HEAD_KV, W.HEAD_DIM, w.n_keys, threads=threads)
-    calls, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        oracle_lib.attn_decode(q, kb, vb, W.N_HEAD, W.N_HEAD_KV, W.HEAD_DIM, w.n_keys, threads=threads)
-        calls += 1
-    dt = (time.perf_counter() - t0) / calls
-    return {"value": round(w.decode_bytes() / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{calls} oracle decode calls at KV 4096 (C3 shape, one layer slice), "
-                      f"{dt * 1e3:.2f} ms/call, {threads} threads over the 24 heads"}
+
+    def call(nt):
+        t = time.perf_counter()
+        oracle_lib.attn_decode(q, kb, vb, W.N_HEAD, W.N_HEAD_KV, W.HEAD_DIM, w.n_keys, threads=nt)
+        return time.perf_counter() - t
+
+    call(threads)
+    times, t0 = [], time.perf_counter()
+    while time.perf_counter() - t0 < seconds or len(times) < 5:
+        times.append(call(threads))
+    dt = statistics.median(times)
+    dt1 = statistics.median([call(1) for _ in range(5)])
+    gbs = lambda t: round(w.decode_bytes() / t / 1e9, 3)
+    return {"value": gbs(dt), "unit": "GB/s", "cores": threads, "kind": "port",
+            "single_thread": {"value": gbs(dt1), "ms_per_call": round(dt1 * 1e3, 2)},
+            "sample": f"median of {len(times)} oracle decode calls at KV 4096 (C3 shape, one layer slice), "
+                      f"{dt * 1e3:.2f} ms/call, {threads} threads over the 24 heads; one thread: median of "
+                      f"5 calls, {dt1 * 1e3:.1f} ms/call"}
+
+
+def probes(torch, W):
+    """Achievable peaks on this box, measured the same way as the kernels: a plain streaming
+    read of the C3 decode bytes (1024 workgroups, 28 rotated copies so the data comes from HBM)
+    and back-to-back f16 MFMAs with no memory traffic (both MFMA shapes the kernels use)."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "inference-agent_amd", "libingot_probe.so"))
+    lib.ingot_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.ingot_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    sink = torch.zeros(1 << 16, device=dev)
+    stream = lambda: ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    n = W.C3.decode_bytes() // 256 * 256
+    buf = torch.ones(28, n // 4, device=dev)
+    rd = time_steps(torch, lambda: [lib.ingot_probe_read(ctypes.c_void_p(buf[i].data_ptr()), n, 1024,
+                                                         ctypes.c_void_p(sink.data_ptr()), stream())
+                                    for i in range(28)], 20, 3, True) / 28
+    del buf
+    out = {"read_C3_bytes": {"us_per_call": round(rd * 1e6, 3), "GB/s": round(n / rd / 1e9, 1),
+                             "bytes": n, "frac_of_8TBs": round(n / rd / 8e12, 4)}}
+    blocks, iters = 1024, 1000
+    for shape, name, mnk in ((0, "mfma_32x32x16_f16", 8 * 32 * 32 * 16), (1, "mfma_16x16x32_f16", 16 * 16 * 16 * 32)):
+        t = time_steps(torch, lambda: lib.ingot_probe_mfma(shape, blocks, iters, ctypes.c_void_p(sink.data_ptr()),
+                                                           stream()), 10, 2, True)
+        flops = blocks * 4 * iters * mnk * 2
+        out[name] = {"TFLOPS": round(flops / t / 1e12, 1), "frac_of_2.5PF": round(flops / t / 2.5e15, 4)}
+    return out
 
 
 def main():
@@ -362,6 +402,9 @@ def main():
             del b
             torch.cuda.empty_cache()
         res["model"][f"Llama-3.2-3B-{t}"] = entry
+
+    if sel in ("all", "probes"):
+        res["probes"] = probes(torch, W)
 
     cpu = None if args.no_cpu else cpu_baseline(W, args.cpu_seconds)
 

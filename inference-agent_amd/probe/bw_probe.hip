@@ -5,6 +5,9 @@
 //   probe_read: each workgroup sums a contiguous chunk of `bytes` with 16-byte loads and writes
 //               one float, so the kernel's HBM traffic is `bytes` read.
 //   probe_copy: dst = src, 16-byte loads and stores (known FETCH_SIZE and WRITE_SIZE).
+//   probe_mfma: back-to-back f16 MFMAs with no memory traffic (independent accumulator chains
+//               per wave: 8 of 32x32x16 or 16 of 16x16x32), the achievable matrix-core rate that the
+//               prefill kernels are measured against next to the 2.5 PFLOP/s spec figure.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -30,6 +33,41 @@ __global__ __launch_bounds__(256) void probe_copy(const float4v* __restrict__ sr
                                                   float4v* __restrict__ dst, size_t n4) {
     for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n4; i += size_t(gridDim.x) * 256)
         dst[i] = src[i];
+}
+
+typedef _Float16 half8p __attribute__((ext_vector_type(8)));
+typedef float float16p __attribute__((ext_vector_type(16)));
+
+template <int SHAPE>  // 0: 32x32x16, 1: 16x16x32
+__global__ __launch_bounds__(256) void probe_mfma(float* __restrict__ sink, int iters) {
+    const half8p a = half8p{} + _Float16(0.001f * (threadIdx.x % 7));
+    const half8p b = half8p{} + _Float16(0.002f * (threadIdx.x % 5));
+    float s = 0.f;
+    if constexpr (SHAPE == 0) {
+        float16p acc[8];
+        for (int c = 0; c < 8; c++) acc[c] = float16p{};
+        for (int i = 0; i < iters; i++)
+#pragma unroll
+            for (int c = 0; c < 8; c++) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+        for (int c = 0; c < 8; c++) s += acc[c][0];
+    } else {
+        float4v acc[16];
+        for (int c = 0; c < 16; c++) acc[c] = float4v{};
+        for (int i = 0; i < iters; i++)
+#pragma unroll
+            for (int c = 0; c < 16; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[c], 0, 0, 0);
+        for (int c = 0; c < 16; c++) s += acc[c][0];
+    }
+    if (s == 12345.678f) sink[blockIdx.x] = s;  // practically never: keeps the chains alive
+}
+
+// FLOPs of one launch: blocks * 4 waves * iters * (8 * 32*32*16 or 16 * 16*16*32) * 2.
+extern "C" int ingot_probe_mfma(int shape, uint32_t n_blocks, int iters, float* sink, void* stream) {
+    if (shape == 0)
+        hipLaunchKernelGGL(probe_mfma<0>, dim3(n_blocks), dim3(256), 0, static_cast<hipStream_t>(stream), sink, iters);
+    else
+        hipLaunchKernelGGL(probe_mfma<1>, dim3(n_blocks), dim3(256), 0, static_cast<hipStream_t>(stream), sink, iters);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
 extern "C" int ingot_probe_read(const void* src, size_t bytes, uint32_t n_blocks, float* sink,
