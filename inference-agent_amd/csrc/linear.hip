@@ -799,7 +799,7 @@ int launch_mv_epi(const MvArgs& a, int epi, uint32_t blocks, size_t lds, hipStre
         case kEpiStore: return launch_mv<T, R, PRO, kEpiStore>(a, blocks, lds, stream);
         case kEpiAccumulate: return launch_mv<T, R, PRO, kEpiAccumulate>(a, blocks, lds, stream);
         default:
-            if constexpr (R == 4) return launch_mv<T, R, PRO, kEpiSiluGate>(a, blocks, lds, stream);
+            if constexpr (R <= 4) return launch_mv<T, R, PRO, kEpiSiluGate>(a, blocks, lds, stream);
             return -2;
     }
 }
@@ -816,8 +816,10 @@ int launch_matvec_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t str
     // (measured: fewer, larger workgroups are slower here; more rows per workgroup only pay
     // for x traffic, which is not the limit) and the rows fit the staging buffer; four
     // otherwise. The gate/up pair takes four of each.
+    // (One row per workgroup when four do not fit: long rows, e.g. a 28672-wide down projection.)
     int R = 4;
     if (epi != kEpiSiluGate && rows / 8 >= 768 && matvec_lds<T>(n_in, a.row_bytes, 8, pro, epi) <= kMvLdsBytes) R = 8;
+    if (matvec_lds<T>(n_in, a.row_bytes, R, pro, epi) > kMvLdsBytes) R = 1;
     const size_t lds = matvec_lds<T>(n_in, a.row_bytes, R, pro, epi);
     if (lds > kMvLdsBytes) return -2;  // rows too long to stage
     uint32_t blocks = 0;
@@ -826,10 +828,13 @@ int launch_matvec_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t str
         a.blk_end[m] = blocks;
     }
     if (epi == kEpiSiluGate) blocks = a.blk_end[0];
-    if (pro == kProRmsNorm) return R == 8 ? launch_mv_epi<T, 8, kProRmsNorm>(a, epi, blocks, lds, stream)
-                                          : launch_mv_epi<T, 4, kProRmsNorm>(a, epi, blocks, lds, stream);
+    if (pro == kProRmsNorm)
+        return R == 8 ? launch_mv_epi<T, 8, kProRmsNorm>(a, epi, blocks, lds, stream)
+             : R == 4 ? launch_mv_epi<T, 4, kProRmsNorm>(a, epi, blocks, lds, stream)
+                      : launch_mv_epi<T, 1, kProRmsNorm>(a, epi, blocks, lds, stream);
     return R == 8 ? launch_mv_epi<T, 8, kProNone>(a, epi, blocks, lds, stream)
-                  : launch_mv_epi<T, 4, kProNone>(a, epi, blocks, lds, stream);
+         : R == 4 ? launch_mv_epi<T, 4, kProNone>(a, epi, blocks, lds, stream)
+                  : launch_mv_epi<T, 1, kProNone>(a, epi, blocks, lds, stream);
 }
 
 // ---------------------------------------------------------------- several tokens

@@ -86,6 +86,17 @@ def test_matvec(dev, oracle_mod, t, n_in, n_out):
 
 
 @pytest.mark.parametrize("t", TYPES)
+def test_matvec_long_rows(dev, oracle_mod, t):
+    """A 28672-wide row (a 70B-class down projection): x alone takes 112 KB of the staging LDS,
+    so the staged kernel falls back to one row per workgroup."""
+    n_in, n_out = 28672, 67
+    raw = gb.random_weights(t, n_out, n_in, seed=5)
+    x = _x(1, n_in, seed=6)
+    got, _ = _run(dev, t, raw, x, n_in, n_out)
+    _close(got, oracle_mod.linear(t, raw, x, n_in, n_out), f"{t} matvec {n_in}x{n_out}")
+
+
+@pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("n_tok,n_in,n_out", [(2, 256, 256), (37, 512, 300), (64, 1024, 512),
                                               (130, 768, 257)])
 def test_matmul(dev, oracle_mod, t, n_tok, n_in, n_out):
