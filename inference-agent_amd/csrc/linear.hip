@@ -400,18 +400,41 @@ template <> struct Col<kQ4_1> { static constexpr int ndw = 5, bytes = 20; };
 template <> struct Col<kQ8_0> { static constexpr int ndw = 9, bytes = 34; };
 template <> struct Col<kF16>  { static constexpr int ndw = 16, bytes = 64; };
 template <> struct Col<kBF16> { static constexpr int ndw = 16, bytes = 64; };
+// Q6_K: column c is the 32-element group (h, g) = ((c % 8) / 4, c % 4) of 210-byte block c / 8;
+// the lane loads the windows of its 32 low-bit bytes, its 32 high-bit bytes, its two scales and
+// the block's d.
+template <> struct Col<kQ6_K> { static constexpr int ndw = 20, bytes = 0; };
 
 template <int T>
-constexpr bool kStreamed = T == kQ4_0 || T == kQ4_1 || T == kQ8_0 || T == kF16 || T == kBF16;
+constexpr bool kStreamed = T == kQ4_0 || T == kQ4_1 || T == kQ8_0 || T == kF16 || T == kBF16 || T == kQ6_K;
+
+// Byte offset of column c from the row start.
+template <int T>
+__device__ __forceinline__ uint32_t col_offset(uint32_t c) {
+    if constexpr (T == kQ6_K) return 210 * (c >> 3);
+    else return c * Col<T>::bytes;
+}
 
 // The window of the column at byte offset off (relative to a 16-byte aligned buffer base).
 template <int T>
-__device__ __forceinline__ void col_load(const __amdgpu_buffer_rsrc_t& rs, uint32_t off, uint32_t (&w)[Col<T>::ndw]) {
+__device__ __forceinline__ void col_load(const __amdgpu_buffer_rsrc_t& rs, uint32_t off, uint32_t (&w)[Col<T>::ndw],
+                                         uint32_t c = 0) {
     auto ld4 = [&](uint32_t o, int at) {
         const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, int(o), 0, 0));
         w[at] = v[0]; w[at + 1] = v[1]; w[at + 2] = v[2]; w[at + 3] = v[3];
     };
-    if constexpr (T == kF16 || T == kBF16) {
+    if constexpr (T == kQ6_K) {
+        const uint32_t h = (c >> 2) & 1, g = c & 3;
+        const uint32_t pl = (off + 64 * h + 32 * (g & 1)) & ~3u, ph = (off + 128 + 32 * h) & ~3u;
+        ld4(pl, 0);
+        ld4(pl + 16, 4);
+        w[8] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(pl + 32), 0, 0);
+        ld4(ph, 9);
+        ld4(ph + 16, 13);
+        w[17] = __builtin_amdgcn_raw_buffer_load_b32(rs, int(ph + 32), 0, 0);
+        w[18] = __builtin_amdgcn_raw_buffer_load_b32(rs, int((off + 192 + 8 * h + 2 * g) & ~3u), 0, 0);
+        w[19] = __builtin_amdgcn_raw_buffer_load_b32(rs, int((off + 208) & ~3u), 0, 0);
+    } else if constexpr (T == kF16 || T == kBF16) {
         for (int i = 0; i < 4; i++) ld4(off + 16 * i, 4 * i);
     } else {
         const uint32_t p = off & ~3u;
@@ -445,8 +468,31 @@ __device__ __forceinline__ uint32_t hi_nibbles(uint32_t w) {
 
 // W-row column · x column (32 elements; sx = sum of the x column, shared by the rows).
 template <int T>
-__device__ __forceinline__ float col_dot(const uint32_t (&w)[Col<T>::ndw], uint32_t off, const float4v (&x)[8], float sx) {
-    if constexpr (T == kF16 || T == kBF16) {
+__device__ __forceinline__ float col_dot(const uint32_t (&w)[Col<T>::ndw], uint32_t off, const float4v (&x)[8], float sx,
+                                         uint32_t c = 0, float sx_hi = 0.f) {
+    if constexpr (T == kQ6_K) {
+        // q = (4 low bits from ql: the low nibble for g < 2, else the high one) | (2 bits of qh
+        // at 2g) << 4, an unsigned 0..63 byte; each 16 elements share an int8 scale:
+        // d * (sc_lo * (sum_lo q x - 32 sum_lo x) + sc_hi * (sum_hi q x - 32 sum_hi x)).
+        const uint32_t h = (c >> 2) & 1, g = c & 3;
+        const uint32_t shl_ = (off + 64 * h + 32 * (g & 1)) & 3, shh_ = (off + 128 + 32 * h) & 3;
+        const uint32_t nib = g >= 2 ? 4 : 0, hb = 2 * g;
+        float s_lo = 0.f, s_hi = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t ql = __builtin_amdgcn_alignbyte(w[i + 1], w[i], shl_);
+            const uint32_t qh = __builtin_amdgcn_alignbyte(w[9 + i + 1], w[9 + i], shh_);
+            uint32_t q = ((ql >> nib) & 0x0F0F0F0Fu) | (((qh >> hb) & 0x03030303u) << 4);
+            asm("" : "+v"(q));  // keep the byte conversions as v_cvt_f32_ubyteN
+            if (i < 4) s_lo = fma_u8x4(q, x[i], s_lo);
+            else s_hi = fma_u8x4(q, x[i], s_hi);
+        }
+        const uint32_t scw = w[18] >> (8 * ((off + 192 + 8 * h + 2 * g) & 3));
+        const float sc_lo = float(int8_t(scw & 0xFF)), sc_hi = float(int8_t((scw >> 8) & 0xFF));
+        const float d = f16_bits((w[19] >> (8 * ((off + 208) & 3))) & 0xFFFF);
+        const float t = fmaf(sc_lo, fmaf(-32.f, sx, s_lo), __fmul_rn(sc_hi, fmaf(-32.f, sx_hi, s_hi)));
+        return __fmul_rn(d, t);
+    } else if constexpr (T == kF16 || T == kBF16) {
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -543,7 +589,7 @@ __global__ __launch_bounds__(NT) void linear_stream_kernel(const MvArgs a) {
     auto load = [&](uint32_t step, uint32_t (&b)[RPH][NDW]) {
         const uint32_t c = min(step * 32 + l32, last);
 #pragma unroll
-        for (int i = 0; i < RPH; i++) col_load<T>(rs[i / RPM], roff[i] + c * Col<T>::bytes, b[i]);
+        for (int i = 0; i < RPH; i++) col_load<T>(rs[i / RPM], roff[i] + col_offset<T>(c), b[i], c);
     };
     // x (and the norm weights, unpermuted after it) into LDS. The loads of x's first round go
     // out first, then the first three columns of the rows (they do not depend on x), then x is
@@ -624,17 +670,22 @@ __global__ __launch_bounds__(NT) void linear_stream_kernel(const MvArgs a) {
         float4v xv[8];
 #pragma unroll
         for (int j = 0; j < 8; j++) xv[j] = xl[(c << 3) | (j ^ ((c >> 1) & 7))];
-        float sx = 0.f;
+        float sx = 0.f, sx_hi = 0.f;
         if constexpr (T == kQ4_0 || T == kQ4_1 || T == kQ8_0) {
 #pragma unroll
             for (int j = 0; j < 8; j++) sx += (xv[j][0] + xv[j][1]) + (xv[j][2] + xv[j][3]);
+        } else if constexpr (T == kQ6_K) {  // the two 16-element halves separately
+#pragma unroll
+            for (int j = 0; j < 4; j++) sx += (xv[j][0] + xv[j][1]) + (xv[j][2] + xv[j][3]);
+#pragma unroll
+            for (int j = 4; j < 8; j++) sx_hi += (xv[j][0] + xv[j][1]) + (xv[j][2] + xv[j][3]);
         }
         const bool valid = c0 < ncols;
 #pragma unroll
         for (int i = 0; i < RPH; i++) {
             // explicit roundings: every instantiation (rows per half-wave, prologue, epilogue)
             // sums a row in exactly the same way
-            const float v = col_dot<T>(b[i], roff[i] + c * Col<T>::bytes, xv, sx);
+            const float v = col_dot<T>(b[i], roff[i] + col_offset<T>(c), xv, sx, c, sx_hi);
             acc[i] = __fadd_rn(acc[i], valid ? v : 0.f);
         }
     };
@@ -735,7 +786,9 @@ int launch_st_epi(const MvArgs& a, int epi, uint32_t blocks, size_t lds, hipStre
 template <int T>
 int launch_stream_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t stream) {
     const bool silu = epi == kEpiSiluGate;
-    constexpr int kMaxRph = T == kF16 || T == kBF16 ? 2 : 4;
+    // (Q6_K: 20-dword windows; two rows per half-wave only where an epilogue needs row pairs,
+    // and then in 256-thread workgroups, whose register budget holds them without spilling)
+    constexpr int kMaxRph = T == kQ6_K ? 1 : T == kF16 || T == kBF16 ? 2 : 4;
     const int min_rph = silu || epi == kEpiRopeKv ? 2 : 1;
     auto count = [&](int nt, int rph, bool set) {
         const uint32_t rpw = uint32_t(nt / 32) * uint32_t(silu ? rph / 2 : rph);  // rows per workgroup
@@ -755,6 +808,7 @@ int launch_stream_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t str
     }
     for (int r = kMaxRph; r >= min_rph && !nt; r /= 2)
         if (count(256, r, false) >= 256 || r == min_rph) { nt = 256; rph = r; }
+    if (!nt) { nt = 256; rph = min_rph; }  // (Q6_K pairs: min_rph above kMaxRph)
     const uint32_t blocks = count(nt, rph, true);
     const size_t lds = size_t(a.n_in) * 4 * (pro == kProRmsNorm ? 2 : 1) + 16;
     if (lds > kMvLdsBytes) return -2;
@@ -762,7 +816,7 @@ int launch_stream_t(MvArgs a, uint32_t n_mats, int pro, int epi, hipStream_t str
         constexpr int P = decltype(pro_tag)::value, N = decltype(nt_tag)::value;
         switch (rph) {
             case 4: if constexpr (kMaxRph >= 4) return launch_st_epi<T, 4, P, N>(a, epi, blocks, lds, stream); return -2;
-            case 2: return launch_st_epi<T, 2, P, N>(a, epi, blocks, lds, stream);
+            case 2: if constexpr (kMaxRph >= 2 || N == 256) return launch_st_epi<T, 2, P, N>(a, epi, blocks, lds, stream); return -2;
             default: return launch_st_epi<T, 1, P, N>(a, epi, blocks, lds, stream);
         }
     };
@@ -1382,7 +1436,7 @@ int launch_proj(uint32_t type, const void* const* W, const float* x, const float
     MvArgs a{};
     if (epi == kEpiRopeKv) {
         if (!rope || n_mats != 3) return -2;
-        if (!(type == kQ4_0 || type == kQ4_1 || type == kQ8_0 || type == kF16 || type == kBF16)) return -2;
+        if (!(type == kQ4_0 || type == kQ4_1 || type == kQ8_0 || type == kF16 || type == kBF16 || type == kQ6_K)) return -2;
         a.inv_freq = rope->inv_freq;
         a.cache[0] = rope->k_row;
         a.cache[1] = rope->v_row;
