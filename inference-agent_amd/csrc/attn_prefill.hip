@@ -73,7 +73,7 @@ __global__ __launch_bounds__(64 * QW * KG) __attribute__((amdgpu_waves_per_eu(G 
 void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict__ K,
                          const _Float16* __restrict__ V, float* __restrict__ out,
                          float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
-                         uint32_t n_head_kv, uint32_t tps, float qscale) {
+                         uint32_t n_head_kv, uint32_t kv_div, uint32_t tps, float qscale) {
     extern __shared__ __attribute__((aligned(16))) char smem[];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -86,8 +86,11 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // block j sees ntiles_j key tiles and is split into n_splits_j = ceil(ntiles_j / tps)
     // near-equal key ranges, so no workgroup walks more than tps tiles (the causal chunk's last
     // block no longer sets the critical path alone).
+    // With kv_div > 1 the G query heads of a unit are a 1/kv_div share of a KV head's group
+    // (n_head_kv counts units, kv_div of them per KV head): the group's heads run in separate
+    // workgroups, each reading the same K/V.
     const uint32_t kvh = blockIdx.x % n_head_kv;
-    const size_t kv_dim = size_t(n_head_kv) * kHeadDim;
+    const size_t kv_dim = size_t(n_head_kv / kv_div) * kHeadDim;
     uint32_t qblk = (n_tok + 16 * QW - 1) / (16 * QW), split = blockIdx.x / n_head_kv, n_splits = 1;
     uint32_t ntiles = 0;
     while (qblk > 0) {
@@ -110,8 +113,8 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     const uint32_t kend_w = q0 < n_tok ? pos + min(n_tok, q0 + 16) : 0;
     const uint32_t qpos = pos + q0 + li;  // this lane's query position
 
-    const _Float16* Kg = K + size_t(kvh) * kHeadDim;
-    const _Float16* Vg = V + size_t(kvh) * kHeadDim;
+    const _Float16* Kg = K + size_t(kvh / kv_div) * kHeadDim;
+    const _Float16* Vg = V + size_t(kvh / kv_div) * kHeadDim;
 
     // Tile copy HBM -> LDS: 32 buffer_load ... lds instructions of 1 KB (4 rows) per tile,
     // spread over the waves of the key group and issued in four parts between the compute
@@ -515,7 +518,7 @@ constexpr int kKG = 2;  // key groups per workgroup (alternate tiles, merged thr
 template <int G>
 int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
-                     uint32_t n_splits, float qscale, hipStream_t stream) {
+                     uint32_t kv_div, uint32_t n_splits, float qscale, hipStream_t stream) {
     static_assert(16 * kQW == kQBlock, "query block size");
     const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
     const uint32_t tps = (max_tiles + n_splits - 1) / n_splits;  // tiles per split at most
@@ -532,7 +535,7 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
         hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
     if (attr != hipSuccess) return -4;
     hipLaunchKernelGGL((attn_prefill_kernel<G, kQW, kKG>), grid, dim3(64 * kQW * kKG), lds, stream,
-                       q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, tps, qscale);
+                       q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, kv_div, tps, qscale);
     if (hipGetLastError() != hipSuccess) return -4;
     if (n_splits > 1) {
         const uint32_t n_head = n_head_kv * G;
@@ -582,11 +585,20 @@ int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* 
                    uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                    uint32_t group, uint32_t n_splits, float scale, hipStream_t stream) {
     const float qscale = scale * kLog2e;
+    // A chunk that gives fewer workgroups than the chip has CUs and needs no key split runs
+    // every query head of a group in its own workgroup (G = 1 over n_head_kv * group units):
+    // 3x the workgroups at G = 3, each walking its keys with a third of the MFMA and softmax
+    // work per tile, so the causal chunk's longest key walk, which sets the kernel's duration,
+    // is shorter (the K/V tile is then read from L2 once per head instead of once per group).
+    const uint32_t blocks = (n_tok + kQBlock - 1) / kQBlock;
+    if (group > 1 && n_splits == 1 && uint64_t(blocks) * n_head_kv * group <= 256)
+        return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv * group, group,
+                                   1, qscale, stream);
     switch (group) {
-        case 1: return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale, stream);
-        case 2: return launch_prefill_g<2>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale, stream);
-        case 3: return launch_prefill_g<3>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale, stream);
-        case 4: return launch_prefill_g<4>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, n_splits, qscale, stream);
+        case 1: return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
+        case 2: return launch_prefill_g<2>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
+        case 3: return launch_prefill_g<3>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
+        case 4: return launch_prefill_g<4>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
         default: return -2;
     }
 }

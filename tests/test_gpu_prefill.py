@@ -116,6 +116,17 @@ def test_prefill_group_sizes(dev, oracle_mod, n_head, n_head_kv):
     assert_parity(got, want, f"G={n_head // n_head_kv}")
 
 
+@pytest.mark.parametrize("n_head,n_head_kv,n_tok", [(64, 32, 300), (48, 16, 400), (64, 16, 300)])
+def test_prefill_group_sizes_whole_groups(dev, oracle_mod, n_head, n_head_kv, n_tok):
+    """Chunks whose query blocks x query heads exceed the 256 CUs keep a group's heads in one
+    workgroup (the chunks above run one workgroup per query head): G = 2, 3, 4, unsplit."""
+    pos = 40
+    q, kb, vb = _inputs(n_head + n_tok, n_head, n_head_kv, pos, n_tok)
+    got = _run_prefill(dev, q, kb, vb, n_head, n_head_kv, pos, n_tok, n_splits=1)
+    want = oracle_mod.attn_prefill(q, kb, vb, n_head, n_head_kv, HD, pos, n_tok, threads=8)
+    assert_parity(got, want, f"G={n_head // n_head_kv} whole groups")
+
+
 def test_prefill_layer_offset_and_stride(dev, oracle_mod):
     # layer slice 1 of a 3-layer cache (other layers NaN) and a padded q/out row stride
     n_ctx, pos, n_tok = 300, 150, 77
