@@ -566,8 +566,9 @@ uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32
         // The shortest per-workgroup key walk whose workgroups still fit one round of 8-wave
         // workgroups on the 256 CUs (one per CU: 128 KB of LDS each), with >= 8 tiles per
         // split: each split adds a record write (~3 us at C4's 26 MB) and the combine launch,
-        // which shorter walks do not pay back (measured: C2 20.0 us unsplit, 22.0 us with 4
-        // splits of <= 2 tiles).
+        // which shorter walks do not pay back (measured with all G heads per workgroup: C2
+        // 20.0 us unsplit, 22.0 us with 4 splits of <= 2 tiles; unsplit chunks now take the
+        // head split of launch_prefill, 11.9 us).
         constexpr uint32_t kMinSplitTiles = 8;
         s = 1;
         for (uint32_t c = 2; c <= cap; c++) {
