@@ -90,7 +90,10 @@ def test_prefill_c5_sampled_rows(dev, oracle_mod):
 
 
 @pytest.mark.parametrize("pos,n_tok", [(0, 1), (0, 2), (0, 7), (0, 33), (5, 64), (100, 65),
-                                       (63, 1), (64, 31), (1000, 97), (0, 160)])
+                                       (63, 1), (64, 31), (1000, 97), (0, 160),
+                                       # either side of the one-workgroup-per-query-head limit
+                                       # (query blocks x 24 heads <= 256): 240 and 264
+                                       (0, 640), (0, 704)])
 def test_prefill_ragged(dev, oracle_mod, pos, n_tok):
     q, kb, vb = _inputs(pos * 7 + n_tok, H, HKV, pos, n_tok, n_ctx=pos + n_tok + 70)
     got = _run_prefill(dev, q, kb, vb, H, HKV, pos, n_tok)
