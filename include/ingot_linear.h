@@ -108,10 +108,19 @@ typedef struct IngotProjDesc {
     uint32_t prologue;   /* INGOT_PROJ_X or INGOT_PROJ_RMSNORM */
     uint32_t epilogue;   /* INGOT_PROJ_STORE, INGOT_PROJ_ACCUMULATE or INGOT_PROJ_SILU_GATE */
     float eps;           /* rmsnorm epsilon (prologue INGOT_PROJ_RMSNORM) */
+    uint32_t n_tok;      /* tokens: 0 or 1 = one decode token; > 1 = a chunk (see below) */
 } IngotProjDesc;
 
-/*   w       host array of n_mats device pointers to the weight bytes, each 16-byte aligned
- *   x       [n_in] f32, 16-byte aligned
+/* A chunk (n_tok > 1) runs the batched linear-layer kernel over the rows of every matrix in one
+ * launch, without split-K: x is [n_tok][n_in], out[m] is [n_tok][n_out[m]], prologue
+ * INGOT_PROJ_X and epilogue INGOT_PROJ_STORE or INGOT_PROJ_ACCUMULATE only (else
+ * INGOT_ATTN_EUNSUPPORTED). Each out[m] equals that of ingot_linear (n_tok, n_splits = 1) on
+ * matrix m, bit for bit. It replaces the q/k/v encode_linear calls of a chunk
+ * (src/metal_backend.mm:440-442) where the three matrices' row tiles together fill the GPU
+ * better than each alone (Llama-3.2-3B at 512 tokens: 160 tiles of 256 rows x 64 tokens against
+ * 96 + 32 + 32 in three launches).
+ *   w       host array of n_mats device pointers to the weight bytes, each 16-byte aligned
+ *   x       [n_in] f32 ([n_tok][n_in] for a chunk), 16-byte aligned
  *   norm_w  [n_in] f32 rmsnorm weights, 16-byte aligned (INGOT_PROJ_RMSNORM; else ignored)
  *   out     host array of n_mats device pointers, f32 [n_out[m]], 4-byte aligned, not
  *           overlapping x or w (one pointer for INGOT_PROJ_SILU_GATE)

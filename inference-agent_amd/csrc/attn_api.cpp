@@ -94,6 +94,11 @@ int check_proj(const void* const* w, const float* x, const float* norm_w, const 
     for (uint32_t m = 0; m < d->n_mats; m++)
         if (!w[m] || !aligned16(w[m]) || d->n_out[m] == 0) return INGOT_ATTN_EINVAL;
     if (uint64_t(d->n_in) / elems * bytes > 0x7fffffffull) return INGOT_ATTN_EUNSUPPORTED;
+    if (d->n_tok > 1) {  // a chunk: the batched kernel, no prologue or fused epilogue
+        if (d->prologue != INGOT_PROJ_X || d->epilogue > INGOT_PROJ_ACCUMULATE) return INGOT_ATTN_EUNSUPPORTED;
+        for (uint32_t m = 0; m < d->n_mats; m++)
+            if (uint64_t(d->n_tok) * d->n_out[m] > 0xffffffffffffull) return INGOT_ATTN_EINVAL;
+    }
     return INGOT_ATTN_OK;
 }
 
@@ -144,7 +149,8 @@ int ingot_proj(const void* const* w, const float* x, const float* norm_w, float*
         if (!out[m] || (reinterpret_cast<uintptr_t>(out[m]) & 3u) != 0) return INGOT_ATTN_EINVAL;
     const int lrc = ingot::launch_proj(d->type, w, x, norm_w, out, d->n_in, d->n_out, d->n_mats,
                                        int(d->prologue), int(d->epilogue), d->eps,
-                                       static_cast<hipStream_t>(stream));
+                                       static_cast<hipStream_t>(stream), nullptr,
+                                       d->n_tok > 1 ? d->n_tok : 1u);
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
 }
 
@@ -153,7 +159,8 @@ int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w
                        const IngotProjDesc* p, const IngotRopeKvDesc* r, void* stream) {
     const int rc = check_proj(w, x, norm_w, p);
     if (rc) return rc;
-    if (!r || p->n_mats != 3 || p->epilogue != INGOT_PROJ_STORE || r->n_tok != 1) return INGOT_ATTN_EINVAL;
+    if (!r || p->n_mats != 3 || p->epilogue != INGOT_PROJ_STORE || r->n_tok != 1 || p->n_tok > 1)
+        return INGOT_ATTN_EINVAL;
     if (r->n_head == 0 || r->n_head_kv == 0 || r->head_dim == 0) return INGOT_ATTN_EINVAL;
     if (r->head_dim % 4 != 0) return INGOT_ATTN_EUNSUPPORTED;
     const uint64_t qd = uint64_t(r->n_head) * r->head_dim, kvd = uint64_t(r->n_head_kv) * r->head_dim;

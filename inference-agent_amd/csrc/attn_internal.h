@@ -60,7 +60,8 @@ struct ProjRope {
 // Returns 0, -2 (type without a kernel, rows too long to stage) or -4 (launch failed).
 int launch_proj(uint32_t type, const void* const* W, const float* x, const float* aux,
                 float* const* out, uint32_t n_in, const uint32_t* n_out, uint32_t n_mats,
-                int pro, int epi, float eps, hipStream_t stream, const ProjRope* rope = nullptr);
+                int pro, int epi, float eps, hipStream_t stream, const ProjRope* rope = nullptr,
+                uint32_t n_tok = 1);
 // Split count for the batched path (requested: 0 = choose); `workspace_bytes` bounds it.
 uint32_t linear_splits(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t requested,
                        size_t workspace_bytes);

@@ -1069,10 +1069,20 @@ template <> struct Stage<kQ8_0> { static constexpr uint32_t ks = 256, bytes = 27
 template <> struct Stage<kQ4_0> { static constexpr uint32_t ks = 256, bytes = 144, pitch = 144; };
 template <> struct Stage<kQ4_1> { static constexpr uint32_t ks = 256, bytes = 160, pitch = 176; };
 
+// Up to three matrices of one type sharing n_in and x (q/k/v of a chunk) in one launch: their
+// row tiles are numbered one after another, matrix m taking tiles [tile_end[m-1], tile_end[m]);
+// out[m] is [n_tok][n_out[m]].
+struct MmMats {
+    const uint8_t* W[3];
+    float* out[3];
+    uint32_t n_out[3];
+    uint32_t tile_end[2];
+};
+
 template <int T, bool LW>
 __global__ __launch_bounds__(512) void linear_matmul_kernel(
-    const uint8_t* __restrict__ W, const float* __restrict__ x, float* __restrict__ out,
-    uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint32_t row_bytes, uint32_t accumulate,
+    const MmMats mats, const float* __restrict__ x,
+    uint32_t n_in, uint32_t n_tok, uint32_t row_bytes, uint32_t accumulate,
     uint32_t tiles_n, uint32_t tiles_m, uint32_t splits, uint32_t k_per_split, uint32_t per_xcd,
     float* __restrict__ part, unsigned int* __restrict__ counters) {
     // Register rings: W raw bytes DW steps ahead, x DX steps ahead of its LDS double buffer.
@@ -1092,10 +1102,17 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const uint32_t total = tiles_n * tiles_m * splits;
     if (L >= total) return;
     const uint32_t split = L % splits, tt = (L / splits) % tiles_m, rt = L / splits / tiles_m;
+    // This row tile's matrix (selected without indexing the argument arrays, which would put
+    // them in scratch) and its tile index within that matrix.
+    const uint32_t mat = rt < mats.tile_end[0] ? 0u : rt < mats.tile_end[1] ? 1u : 2u;
+    const uint8_t* __restrict__ const W = mat == 0 ? mats.W[0] : mat == 1 ? mats.W[1] : mats.W[2];
+    float* __restrict__ const out = mat == 0 ? mats.out[0] : mat == 1 ? mats.out[1] : mats.out[2];
+    const uint32_t n_out = mat == 0 ? mats.n_out[0] : mat == 1 ? mats.n_out[1] : mats.n_out[2];
+    const uint32_t rtl = rt - (mat == 0 ? 0u : mat == 1 ? mats.tile_end[0] : mats.tile_end[1]);
     const uint32_t kbeg = split * k_per_split;
     const uint32_t steps = (min(n_in, kbeg + k_per_split) - kbeg) / kMmK;
     const uint32_t tok0 = tt * kMmToks;
-    const uint32_t rowbase = rt * kMmRows + wave * kMmRowsWave;
+    const uint32_t rowbase = rtl * kMmRows + wave * kMmRowsWave;
 
     // x staging: thread t converts 4 consecutive k of token t/8. Loads are unconditional (rows
     // past n_tok read the last token, steps past the split re-read its last step; neither
@@ -1132,9 +1149,9 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         __shared__ __attribute__((aligned(16))) _Float16 xst[2][kMmToks * XP];
         extern __shared__ __attribute__((aligned(16))) uint8_t wsm[];  // [2][kMmRows][PITCH]
         const uint32_t nst = steps / P;
-        const uint32_t rows_here = min(n_out - rt * kMmRows, uint32_t(kMmRows));
+        const uint32_t rows_here = min(n_out - rtl * kMmRows, uint32_t(kMmRows));
         const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(W + size_t(rt) * kMmRows * row_bytes), 0, int(rows_here * row_bytes),
+            const_cast<uint8_t*>(W + size_t(rtl) * kMmRows * row_bytes), 0, int(rows_here * row_bytes),
             kBufferFlags);
         const uint32_t kbyte0 = kbeg / Fmt<T>::blk * Fmt<T>::bytes;
         uint32_t goff[NCH], loff[NCH];
@@ -1344,11 +1361,55 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     }
 }
 
+// The batched kernel over mats (n_mats matrices; W, out and n_out set) with `splits`-way
+// split-K (partials and counters in the workspace when splits > 1).
+template <int T>
+int launch_mm_t(MmMats mats, uint32_t n_mats, const float* x, uint32_t n_in, uint32_t n_tok,
+                uint32_t accumulate, uint32_t splits, void* workspace, hipStream_t stream) {
+    const uint32_t row_bytes = n_in / Fmt<T>::blk * Fmt<T>::bytes;
+    uint32_t tiles_n = 0;
+    for (uint32_t m = 0; m < 3; m++) {
+        if (m < n_mats) tiles_n += (mats.n_out[m] + kMmRows - 1) / kMmRows;
+        if (m < 2) mats.tile_end[m] = tiles_n;
+    }
+    const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
+    // LDS-staged W when rows split into whole 16-byte stage pieces.
+    constexpr uint32_t KS = Stage<T>::ks;
+    const bool lw = KS != 0 && row_bytes % 16 == 0 && n_in % (KS != 0 ? KS : 1) == 0;
+    const uint32_t gran = lw ? KS : kMmK;
+    const uint32_t units = n_in / gran;
+    const uint32_t k_per_split = (units + splits - 1) / splits * gran;
+    splits = (n_in + k_per_split - 1) / k_per_split;  // never more than requested
+    const uint64_t total = uint64_t(tiles_n) * tiles_m * splits;
+    const uint64_t per_xcd = (total + 7) / 8;
+    if (per_xcd * 8 > 0x7fffffffu) return -1;
+    auto* counters = static_cast<unsigned int*>(workspace);
+    auto* part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kLinearCounterBytes)
+                            : nullptr;
+    const dim3 grid(uint32_t(per_xcd * 8)), block(kMmWaves * 64);
+    if constexpr (Stage<T>::ks != 0) {
+        if (lw) {
+            const size_t lds = size_t(2) * kMmRows * Stage<T>::pitch;
+            static const hipError_t attr = hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&linear_matmul_kernel<T, true>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
+            if (attr != hipSuccess) return -4;
+            hipLaunchKernelGGL((linear_matmul_kernel<T, true>), grid, block, lds, stream, mats, x,
+                               n_in, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits,
+                               k_per_split, uint32_t(per_xcd), part, counters);
+            return hipGetLastError() == hipSuccess ? 0 : -4;
+        }
+    }
+    hipLaunchKernelGGL((linear_matmul_kernel<T, false>), grid, block, 0, stream, mats, x, n_in,
+                       n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits, k_per_split,
+                       uint32_t(per_xcd), part, counters);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 template <int T>
 int launch_t(const uint8_t* W, const float* x, float* out, uint32_t n_in, uint32_t n_out,
              uint32_t n_tok, uint32_t accumulate, uint32_t n_splits, void* workspace,
              size_t workspace_bytes, hipStream_t stream) {
-    const uint32_t row_bytes = n_in / Fmt<T>::blk * Fmt<T>::bytes;
     if (n_tok == 1) {
         MvArgs a{};
         a.W[0] = W;
@@ -1357,42 +1418,13 @@ int launch_t(const uint8_t* W, const float* x, float* out, uint32_t n_in, uint32
         a.x = x;
         a.n_in = n_in;
         return launch_matvec_t<T>(a, 1, kProNone, accumulate ? kEpiAccumulate : kEpiStore, stream);
-    } else {
-        const uint32_t tiles_n = (n_out + kMmRows - 1) / kMmRows;
-        const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
-        uint32_t splits = workspace ? linear_splits(n_in, n_out, n_tok, n_splits, workspace_bytes) : 1;
-        // LDS-staged W when rows split into whole 16-byte stage pieces.
-        constexpr uint32_t KS = Stage<T>::ks;
-        const bool lw = KS != 0 && row_bytes % 16 == 0 && n_in % (KS != 0 ? KS : 1) == 0;
-        const uint32_t gran = lw ? KS : kMmK;
-        const uint32_t units = n_in / gran;
-        const uint32_t k_per_split = (units + splits - 1) / splits * gran;
-        splits = (n_in + k_per_split - 1) / k_per_split;  // never more than requested
-        const uint64_t total = uint64_t(tiles_n) * tiles_m * splits;
-        const uint64_t per_xcd = (total + 7) / 8;
-        if (per_xcd * 8 > 0x7fffffffu) return -1;
-        auto* counters = static_cast<unsigned int*>(workspace);
-        auto* part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kLinearCounterBytes)
-                                : nullptr;
-        const dim3 grid(uint32_t(per_xcd * 8)), block(kMmWaves * 64);
-        if constexpr (Stage<T>::ks != 0) {
-            if (lw) {
-                const size_t lds = size_t(2) * kMmRows * Stage<T>::pitch;
-                static const hipError_t attr = hipFuncSetAttribute(
-                    reinterpret_cast<const void*>(&linear_matmul_kernel<T, true>),
-                    hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-                if (attr != hipSuccess) return -4;
-                hipLaunchKernelGGL((linear_matmul_kernel<T, true>), grid, block, lds, stream, W, x, out,
-                                   n_in, n_out, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits,
-                                   k_per_split, uint32_t(per_xcd), part, counters);
-                return hipGetLastError() == hipSuccess ? 0 : -4;
-            }
-        }
-        hipLaunchKernelGGL((linear_matmul_kernel<T, false>), grid, block, 0, stream, W, x, out, n_in,
-                           n_out, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits, k_per_split,
-                           uint32_t(per_xcd), part, counters);
     }
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+    MmMats mats{};
+    mats.W[0] = W;
+    mats.out[0] = out;
+    mats.n_out[0] = n_out;
+    const uint32_t splits = workspace ? linear_splits(n_in, n_out, n_tok, n_splits, workspace_bytes) : 1;
+    return launch_mm_t<T>(mats, 1, x, n_in, n_tok, accumulate, splits, workspace, stream);
 }
 
 }  // namespace
@@ -1432,7 +1464,27 @@ size_t linear_workspace_size(uint32_t n_in, uint32_t n_out, uint32_t n_tok, uint
 
 int launch_proj(uint32_t type, const void* const* W, const float* x, const float* aux,
                 float* const* out, uint32_t n_in, const uint32_t* n_out, uint32_t n_mats,
-                int pro, int epi, float eps, hipStream_t stream, const ProjRope* rope) {
+                int pro, int epi, float eps, hipStream_t stream, const ProjRope* rope, uint32_t n_tok) {
+    if (n_tok > 1) {  // a chunk: the batched kernel over every matrix's rows, no split-K
+        if (pro != kProNone || (epi != kEpiStore && epi != kEpiAccumulate) || rope) return -2;
+        MmMats mats{};
+        for (uint32_t m = 0; m < n_mats; m++) {
+            mats.W[m] = static_cast<const uint8_t*>(W[m]);
+            mats.out[m] = out[m];
+            mats.n_out[m] = n_out[m];
+        }
+        const uint32_t acc = epi == kEpiAccumulate ? 1u : 0u;
+        switch (type) {
+            case kF32:  return launch_mm_t<kF32>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            case kF16:  return launch_mm_t<kF16>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            case kBF16: return launch_mm_t<kBF16>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            case kQ8_0: return launch_mm_t<kQ8_0>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            case kQ4_0: return launch_mm_t<kQ4_0>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            case kQ4_1: return launch_mm_t<kQ4_1>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            case kQ6_K: return launch_mm_t<kQ6_K>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            default:    return -2;
+        }
+    }
     MvArgs a{};
     if (epi == kEpiRopeKv) {
         if (!rope || n_mats != 3) return -2;

@@ -151,9 +151,15 @@ public:
                 attn_->proj_kv_store(l, pos, w, x_, L.attn_norm, d, q_, k_, v_);
             } else {
                 abi(ingot_rmsnorm(x_, L.attn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
-                linear(L.wq, h_, q_, ne, qd, un, false);
-                linear(L.wk, h_, k_, ne, kvd, un, false);
-                linear(L.wv, h_, v_, ne, kvd, un, false);
+                if (n > 1 && L.wq.type == L.wk.type && L.wq.type == L.wv.type && qkv_one_launch(un, qd, kvd)) {
+                    const Dev* w[3] = {&L.wq, &L.wk, &L.wv};
+                    float* outs[3] = {q_, k_, v_};
+                    proj(w, 3, h_, nullptr, outs, INGOT_PROJ_X, INGOT_PROJ_STORE, "q/k/v", un);
+                } else {
+                    linear(L.wq, h_, q_, ne, qd, un, false);
+                    linear(L.wk, h_, k_, ne, kvd, un, false);
+                    linear(L.wv, h_, v_, ne, kvd, un, false);
+                }
                 attn_->kv_store(l, pos, n, q_, k_, v_);
             }
             attn_->attention(l, pos, n, q_, attn_out_);
@@ -241,10 +247,18 @@ private:
         IngotLinearDesc d{w.type, w.n_in, w.n_out, n_tok, 0, 0, 0};
         return ingot_linear_workspace_size(&d);
     }
-    // One token through 1..3 matrices sharing x (ingot_proj).
+    // A chunk's q/k/v run as one batched launch (no split-K) rather than three split-K
+    // ingot_linear calls when the three matrices' tiles of 256 rows x 64 tokens reach half the
+    // CUs together (Llama-3.2-3B at 512 tokens: 160 tiles; at 256 tokens 80).
+    static bool qkv_one_launch(uint32_t n_tok, uint32_t q_dim, uint32_t kv_dim) {
+        const uint32_t rows = (q_dim + 255) / 256 + 2 * ((kv_dim + 255) / 256);
+        return uint64_t(rows) * ((n_tok + 63) / 64) >= 128;
+    }
+    // One token (or a chunk of n_tok) through 1..3 matrices sharing x (ingot_proj).
     void proj(const Dev* const* w, uint32_t n_mats, const float* x, const float* norm_w, float* const* outs,
-              uint32_t prologue, uint32_t epilogue, const char* what) {
+              uint32_t prologue, uint32_t epilogue, const char* what, uint32_t n_tok = 1) {
         IngotProjDesc d{};
+        d.n_tok = n_tok;
         d.type = w[0]->type;
         d.n_in = w[0]->n_in;
         d.n_mats = n_mats;

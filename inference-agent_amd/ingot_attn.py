@@ -111,7 +111,8 @@ PROJ_STORE, PROJ_ACCUMULATE, PROJ_SILU_GATE = 0, 1, 2
 
 class ProjDesc(ctypes.Structure):
     """IngotProjDesc: one decode token through up to three matrices sharing x, with the
-    rmsnorm before and the residual add / silu gate after fused in."""
+    rmsnorm before and the residual add / silu gate after fused in; or (n_tok > 1) a chunk
+    through up to three matrices in one batched launch (store / accumulate only)."""
 
     _fields_ = [
         ("type", c_uint32),
@@ -121,6 +122,7 @@ class ProjDesc(ctypes.Structure):
         ("prologue", c_uint32),
         ("epilogue", c_uint32),
         ("eps", c_float),
+        ("n_tok", c_uint32),
     ]
 
 
@@ -340,15 +342,15 @@ def linear(w, x, out, desc: LinearDesc, stream=None, workspace=None, use_workspa
     return out
 
 
-def proj_desc(type_, n_in, n_out, prologue=PROJ_X, epilogue=PROJ_STORE, eps=0.0):
+def proj_desc(type_, n_in, n_out, prologue=PROJ_X, epilogue=PROJ_STORE, eps=0.0, n_tok=1):
     t = GGUF_TYPES[type_] if isinstance(type_, str) else int(type_)
     n_out = list(n_out)
     return ProjDesc(t, n_in, len(n_out), (c_uint32 * 3)(*(n_out + [0] * (3 - len(n_out)))),
-                    prologue, epilogue, eps)
+                    prologue, epilogue, eps, n_tok)
 
 
 def proj(ws, x, outs, desc: ProjDesc, norm_w=None, stream=None):
-    """One token: out[m] (+)= W[m]·x' for the weight-byte tensors `ws`, x' = x or
+    """One token (or a chunk, desc.n_tok > 1): out[m] (+)= W[m]·x' for the weight-byte tensors `ws`, x' = x or
     rmsnorm(x) * norm_w; with PROJ_SILU_GATE (ws = [gate, up]) outs[0] = silu(gate·x') * (up·x').
     The fused form of rmsnorm + encode_linear (+ encode_silu_mul) (src/metal_backend.mm:433-452)."""
     n = len(ws)

@@ -22,6 +22,15 @@ import numpy as np
 import ingot_attn as ia
 
 
+def qkv_one_launch(n_tok, q_dim, kv_dim):
+    """Whether a chunk's q/k/v run as one batched launch (ingot_proj, no split-K) rather than
+    three ingot_linear calls (each split-K over the 256 CUs): when the three matrices' tiles of
+    256 rows x 64 tokens reach half the CUs together (Llama-3.2-3B at 512 tokens: 160 tiles; at
+    256 tokens 80, where three split launches are faster)."""
+    rows = -(-q_dim // 256) + 2 * -(-kv_dim // 256)
+    return rows * -(-n_tok // 64) >= 128
+
+
 class HipForward:
     def __init__(self, model: dict, n_ctx: int, n_batch: int, device="cuda:0"):
         import torch
@@ -100,9 +109,13 @@ class HipForward:
                                 rope, norm_w=L["attn_norm"])
             else:
                 ia.rmsnorm(self.x, L["attn_norm"], self.h, ne, n, eps)
-                self._lin(L["wq"], self.h, self.q, ne, qd, n)
-                self._lin(L["wk"], self.h, self.k, ne, kvd, n)
-                self._lin(L["wv"], self.h, self.v, ne, kvd, n)
+                if n > 1 and L["wq"][0] == L["wk"][0] == L["wv"][0] and qkv_one_launch(n, qd, kvd):
+                    ia.proj([L["wq"][1], L["wk"][1], L["wv"][1]], self.h, [self.q, self.k, self.v],
+                            ia.proj_desc(L["wq"][0], ne, [qd, kvd, kvd], n_tok=n))
+                else:
+                    self._lin(L["wq"], self.h, self.q, ne, qd, n)
+                    self._lin(L["wk"], self.h, self.k, ne, kvd, n)
+                    self._lin(L["wv"], self.h, self.v, ne, kvd, n)
                 ia.rope_kv_store(self.q, self.k, self.v, self.k_cache, self.v_cache, self.inv_freq, rope)
             kv_offset = l * self.n_ctx * kvd
             if n == 1:

@@ -71,8 +71,9 @@ def test_struct_layout_matches_c():
                offsetof(IngotRopeKvDesc, q_stride), offsetof(IngotRopeKvDesc, kv_stride));
         printf("%zu %zu %zu\n", sizeof(IngotLinearDesc), offsetof(IngotLinearDesc, accumulate),
                offsetof(IngotLinearDesc, n_splits));
-        printf("%zu %zu %zu %zu\n", sizeof(IngotProjDesc), offsetof(IngotProjDesc, n_out),
-               offsetof(IngotProjDesc, epilogue), offsetof(IngotProjDesc, eps));
+        printf("%zu %zu %zu %zu %zu\n", sizeof(IngotProjDesc), offsetof(IngotProjDesc, n_out),
+               offsetof(IngotProjDesc, epilogue), offsetof(IngotProjDesc, eps),
+               offsetof(IngotProjDesc, n_tok));
         printf("%d %d %d %d %d\n", INGOT_PROJ_X, INGOT_PROJ_RMSNORM, INGOT_PROJ_STORE,
                INGOT_PROJ_ACCUMULATE, INGOT_PROJ_SILU_GATE);
         return 0;
@@ -90,7 +91,7 @@ def test_struct_layout_matches_c():
                     P.kv_offset.offset, P.q_stride.offset, P.scale.offset, ctypes.sizeof(R),
                     R.dst_offset.offset, R.q_stride.offset, R.kv_stride.offset, ctypes.sizeof(Li),
                     Li.accumulate.offset, Li.n_splits.offset, ctypes.sizeof(Pj), Pj.n_out.offset,
-                    Pj.epilogue.offset, Pj.eps.offset, ingot_attn.PROJ_X, ingot_attn.PROJ_RMSNORM,
+                    Pj.epilogue.offset, Pj.eps.offset, Pj.n_tok.offset, ingot_attn.PROJ_X, ingot_attn.PROJ_RMSNORM,
                     ingot_attn.PROJ_STORE, ingot_attn.PROJ_ACCUMULATE, ingot_attn.PROJ_SILU_GATE]
 
 
@@ -217,6 +218,9 @@ def test_proj_descriptor_checks(lib):
     assert call(ia.proj_desc("F16", 256, [4], epilogue=2)) == -1
     assert call(ia.proj_desc("F16", 256, [4, 8], epilogue=2)) == -1
     assert call(ia.proj_desc("F16", 256, [4, 4, 4], epilogue=2)) == -1
+    # a chunk takes no rmsnorm prologue and no silu epilogue
+    assert call(ia.proj_desc("F16", 256, [4], prologue=1, eps=1e-5, n_tok=5)) == -2
+    assert call(ia.proj_desc("F16", 256, [4, 4], epilogue=2, n_tok=5)) == -2
 
 
 def test_proj_rope_kv_checks(lib):
@@ -238,6 +242,7 @@ def test_proj_rope_kv_checks(lib):
     assert call(p=ia.proj_desc("Q4_0", 3072, [3072, 1024, 1024], epilogue=1)) == -1
     assert call(p=ia.proj_desc("Q4_0", 3072, [3072, 1024, 512])) == -1        # v rows != kv dim
     assert call(r=ia.rope_kv_desc(24, 8, 128, 5, 2)) == -1                      # one token only
+    assert call(p=ia.proj_desc("Q4_0", 3072, [3072, 1024, 1024], n_tok=2)) == -1
     assert call(r=ia.rope_kv_desc(24, 8, 130, 5, 1)) in (-1, -2)                # head_dim % 4
     assert call(q=None) == -1 and call(kc=None) == -1 and call(inv=None) == -1
     assert call(q=P((1 << 20) + 4)) == -1                                       # q alignment

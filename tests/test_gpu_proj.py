@@ -188,3 +188,47 @@ def test_proj_rope_kv(dev, t, pos):
     untouched[pos] = False
     assert bool((kc1.view(torch.int16)[untouched] == 0x7E00).all())
     assert bool((vc1.view(torch.int16)[untouched] == 0x7E00).all())
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_tok,n_in,n_outs,acc", [(512, 3072, (3072, 1024, 1024), False),
+                                                   (70, 512, (200, 77, 3), False),
+                                                   (130, 768, (257, 513), True)])
+def test_chunk_matrices_one_launch(dev, oracle_mod, t, n_tok, n_in, n_outs, acc):
+    """A chunk (n_tok > 1) through up to three matrices in one batched launch: each output
+    equals ingot_linear on its matrix (same n_tok, n_splits = 1) bit for bit, the f16-rounding
+    oracle (oracle_linear_f16) on sampled token rows within the matmul bar (rel-L2 <= 1e-5,
+    max|d| <= 1e-5 * max|ref| + 1e-6), and nothing past a matrix's [n_tok][n_out] is written."""
+    import torch
+    import ingot_attn as ia
+
+    rng = np.random.default_rng(n_tok + n_in)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    raws = [gb.random_weights(t, n, n_in, seed=n_in + 7 * i + 1) for i, n in enumerate(n_outs)]
+    bases = [rng.standard_normal((n_tok, n)).astype(np.float32) if acc else None for n in n_outs]
+    pad = 29
+
+    def fresh(i):
+        buf = np.full(n_tok * n_outs[i] + pad, np.nan, np.float32)
+        if acc:
+            buf[: n_tok * n_outs[i]] = bases[i].ravel()
+        return _t(buf, dev)
+
+    xd = _t(x, dev)
+    wd = [_t(r.reshape(-1), dev) for r in raws]
+    outs = [fresh(i) for i in range(len(n_outs))]
+    ia.proj(wd, xd, outs, ia.proj_desc(t, n_in, list(n_outs), epilogue=ia.PROJ_ACCUMULATE if acc else ia.PROJ_STORE,
+                                       n_tok=n_tok))
+    refs = [fresh(i) for i in range(len(n_outs))]
+    for w, r, n in zip(wd, refs, n_outs):
+        ia.linear(w, xd, r, ia.linear_desc(t, n_in, n, n_tok, accumulate=acc, n_splits=1), use_workspace=False)
+    torch.cuda.synchronize()
+    rows = sorted({0, 1, n_tok // 2, n_tok - 2, n_tok - 1})
+    for i, (o, r, raw, n) in enumerate(zip(outs, refs, raws, n_outs)):
+        got = o.cpu().numpy()
+        assert np.array_equal(got, r.cpu().numpy(), equal_nan=True), f"{t} matrix {i}: != ingot_linear"
+        assert np.all(np.isnan(got[n_tok * n:])), f"{t} matrix {i}: wrote past its rows"
+        got = got[: n_tok * n].reshape(n_tok, n)[rows]
+        base = bases[i][rows] if acc else None
+        want = oracle_mod.linear(t, raw, x[rows], n_in, n, out=base, accumulate=acc, f16_path=True)
+        _close(got, want, f"{t} chunk {n_tok}x{n_in}x{n} matrix {i}")
