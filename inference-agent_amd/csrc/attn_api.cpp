@@ -18,23 +18,34 @@ namespace {
 using ingot::kCounterBytes;
 constexpr size_t kPartFloats = 132;     // per-(split, head) partial record, as in the kernels
 
+size_t prefill_part_offset(uint32_t n_head) { return kCounterBytes + size_t(n_head) * ingot::kDecodeHeadRecordBytes; }
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-int check_common(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
+int check_heads(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
     if (n_head == 0 || n_head_kv == 0 || head_dim == 0) return INGOT_ATTN_EINVAL;
     if (n_head % n_head_kv != 0) return INGOT_ATTN_EINVAL;
-    if (head_dim != 128) return INGOT_ATTN_EUNSUPPORTED;
-    const uint32_t group = n_head / n_head_kv;
-    if (group < 1 || group > 4) return INGOT_ATTN_EUNSUPPORTED;
-    // One completion counter per query head (decode) or KV head (prefill).
+    // One epoch word per query head in the workspace.
     if (n_head > kCounterBytes / (ingot::kCounterStride * sizeof(unsigned int))) return INGOT_ATTN_EUNSUPPORTED;
     return INGOT_ATTN_OK;
 }
 
+// Prefill: head_dim 128 and n_head / n_head_kv in 1..4 (the MFMA prefill kernel's envelope).
+int check_common(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
+    const int rc = check_heads(n_head, n_head_kv, head_dim);
+    if (rc) return rc;
+    if (head_dim != 128) return INGOT_ATTN_EUNSUPPORTED;
+    const uint32_t group = n_head / n_head_kv;
+    if (group < 1 || group > 4) return INGOT_ATTN_EUNSUPPORTED;
+    return INGOT_ATTN_OK;
+}
+
+// Decode: head_dim 64, 128 or 256, any group size.
 int check_decode(const IngotAttnDecodeDesc* d) {
     if (!d) return INGOT_ATTN_EINVAL;
-    const int rc = check_common(d->n_head, d->n_head_kv, d->head_dim);
+    const int rc = check_heads(d->n_head, d->n_head_kv, d->head_dim);
     if (rc) return rc;
+    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return INGOT_ATTN_EUNSUPPORTED;
     if (d->n_keys == 0 || d->kv_offset % 8 != 0) return INGOT_ATTN_EINVAL;
     if (!(d->scale > 0.f)) return INGOT_ATTN_EINVAL;
     return INGOT_ATTN_OK;
@@ -190,7 +201,7 @@ int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w
 
 uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
     if (check_decode(d)) return 0;
-    return ingot::decode_splits(d->n_keys, d->n_head_kv, d->n_splits);
+    return ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
 }
 
 uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
@@ -200,15 +211,17 @@ uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
 
 size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
     if (check_decode(d)) return 0;
-    const uint32_t splits = ingot::decode_splits(d->n_keys, d->n_head_kv, d->n_splits);
-    return kCounterBytes + size_t(splits) * d->n_head * kPartFloats * sizeof(float);
+    const uint32_t splits = ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
+    return kCounterBytes + (splits > 1 ? size_t(d->n_head) * ingot::kDecodeHeadRecordBytes : 0);
 }
 
 size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d) {
     if (check_prefill(d)) return 0;
     const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
     const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head * kPartFloats * sizeof(float) : 0;
-    return kCounterBytes + parts;
+    // The prefill records follow the decode record regions of the same heads, so a workspace
+    // shared by decode and prefill calls never holds prefill data where decode tags are read.
+    return prefill_part_offset(d->n_head) + parts;
 }
 
 int ingot_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
@@ -221,15 +234,14 @@ int ingot_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
         !aligned16(workspace))
         return INGOT_ATTN_EINVAL;
     if (workspace_bytes < ingot_attn_decode_workspace_size(d)) return INGOT_ATTN_EWORKSPACE;
-    const uint32_t splits = ingot::decode_splits(d->n_keys, d->n_head_kv, d->n_splits);
-    auto* counters = static_cast<unsigned int*>(workspace);
-    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    const uint32_t splits = ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
     const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
-    const int lrc = ingot::launch_decode(q, k, v, out, part, counters, d->n_keys, splits,
-                                         d->n_head_kv, d->n_head / d->n_head_kv, d->scale,
+    const int lrc = ingot::launch_decode(q, k, v, out, workspace, d->n_keys, splits, d->n_head_kv,
+                                         d->n_head / d->n_head_kv, d->head_dim, d->scale,
                                          static_cast<hipStream_t>(stream));
-    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
+         : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
 
 int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, float* out,
@@ -243,7 +255,7 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
         return INGOT_ATTN_EINVAL;
     if (workspace_bytes < ingot_attn_prefill_workspace_size(d)) return INGOT_ATTN_EWORKSPACE;
     const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
-    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes);
+    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_part_offset(d->n_head));
     const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
     const int lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride,
@@ -308,7 +320,7 @@ const char* ingot_attn_strerror(int code) {
     switch (code) {
         case INGOT_ATTN_OK: return "ok";
         case INGOT_ATTN_EINVAL: return "invalid argument (null/misaligned pointer, zero size or position out of range)";
-        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (attention: head_dim 128, n_head/n_head_kv in 1..4, n_head <= 256; linear: weight type without a kernel or n_in not a multiple of its block)";
+        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (decode: head_dim 64/128/256; prefill: head_dim 128 and n_head/n_head_kv in 1..4; n_head <= 256; linear: weight type without a kernel or n_in not a multiple of its block)";
         case INGOT_ATTN_EWORKSPACE: return "workspace smaller than the *_workspace_size() figure";
         case INGOT_ATTN_EHIP: return "HIP launch failed";
         default: return "unknown error";

@@ -1,4 +1,6 @@
-// attn_decode.hip — split-KV (flash-decoding) GQA decode attention for gfx950.
+// attn_decode.hip — split-KV (flash-decoding) GQA decode attention for gfx950: the tuned kernel
+// for head_dim 128 and groups 1..4 (Llama-3.2-3B: group 3); attn_decode_any.hip serves the other
+// shapes.
 //
 // Computes, for one query token and every Q head h, out_h = softmax(q_h K^T * scale) V over cache
 // rows 0..n_keys-1 of KV head h / G — the attention block of src/cpu_backend.cpp:51-69 and the
@@ -308,27 +310,12 @@ void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Floa
 }
 
 constexpr int kNW = 4;
-constexpr uint32_t kMinKeysPerSplit = 32;  // two wave steps: the tail costs more than the loads
-constexpr uint32_t kOneSplitKeys = 192;
 
 }  // namespace
 
-uint32_t decode_splits(uint32_t n_keys, uint32_t n_head_kv, uint32_t requested) {
-    (void)n_head_kv;
-    uint32_t splits = requested;
-    // Short caches take one workgroup per KV head: below ~192 keys the split records, counter
-    // and merge cost more than the parallel key walk saves (measured at 129 keys: 4.6 us in one
-    // split, 5.0 us in five).
-    if (splits == 0) splits = n_keys <= kOneSplitKeys ? 1 : (n_keys + kMinKeysPerSplit - 1) / kMinKeysPerSplit;
-    splits = max(1u, min(splits, min(n_keys, kMaxDecodeSplits)));
-    // No empty splits: recompute from the per-split key count.
-    const uint32_t per = (n_keys + splits - 1) / splits;
-    return (n_keys + per - 1) / per;
-}
-
-int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
-                  unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
-                  uint32_t group, float scale, hipStream_t stream) {
+int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+                       unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
+                       uint32_t group, float scale, hipStream_t stream) {
     const uint32_t per = (n_keys + n_splits - 1) / n_splits;
     const uint32_t blocks = n_splits * n_head_kv;
     const float qscale = scale * kLog2e;

@@ -16,13 +16,35 @@ constexpr uint32_t kMaxPrefillSplits = 16;
 constexpr uint32_t kCounterStride = 64;  // uint32 words
 constexpr size_t kCounterBytes = 65536;  // up to 256 heads
 
-uint32_t decode_splits(uint32_t n_keys, uint32_t n_head_kv, uint32_t requested);
+// Decode: split count for n_keys (requested 0 = choose), the most splits a head_dim allows, and
+// the query heads one workgroup serves for a group size (a divisor of it, at most 8).
+uint32_t decode_splits(uint32_t n_keys, uint32_t head_dim, uint32_t requested);
+uint32_t decode_max_splits(uint32_t head_dim);
+uint32_t decode_unit_heads(uint32_t group);
+// Bytes of one decode split record of the generic kernel: o[head_dim] as f32 and one 16-byte
+// {m, l, flag, flag} chunk; and the fixed region per query head that holds all records of a call
+// (the largest of max splits x record bytes over head_dim 64 / 128 / 256: 32 x 528), which also
+// holds the head_dim-128 kernel's records ([head][split][132] floats).
+constexpr uint32_t decode_record_bytes(uint32_t head_dim) { return head_dim * 4 + 16; }
+constexpr size_t kDecodeHeadRecordBytes = 32 * 528;
+static_assert(kDecodeHeadRecordBytes >= 32 * decode_record_bytes(64) &&
+              kDecodeHeadRecordBytes >= 32 * decode_record_bytes(128) &&
+              kDecodeHeadRecordBytes >= 16 * decode_record_bytes(256), "decode record region");
 uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t requested);
 
-// Return 0, -2 (unsupported group) or -4 (launch failed).
-int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
-                  unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
-                  uint32_t group, float scale, hipStream_t stream);
+// Decode attention, dispatched by launch_decode: head_dim 128 with groups 1..4 take the tuned
+// kernel (attn_decode.hip; completion counters in the workspace's first kCounterBytes, records
+// after them), every other shape the generic one (attn_decode_any.hip; records after the first
+// kCounterBytes). Return 0, -1 (grid too large), -2 (shape without a kernel) or -4 (launch failed).
+int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* out, void* workspace,
+                  uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
+                  uint32_t head_dim, float scale, hipStream_t stream);
+int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+                       unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
+                       uint32_t group, float scale, hipStream_t stream);
+int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, float* out, void* recs,
+                      uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
+                      uint32_t head_dim, float scale, hipStream_t stream);
 int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
                    uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                    uint32_t group, uint32_t n_splits, float scale, hipStream_t stream);

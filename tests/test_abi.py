@@ -101,17 +101,26 @@ def test_host_validation(lib):
     ok = ia.decode_desc(24, 8, 128, 4096)
     assert lib.ingot_attn_decode_workspace_size(ctypes.byref(ok)) > 0
     assert ia.decode_splits(ok) >= 1
-    for bad in (ia.decode_desc(24, 8, 64, 4096),   # head_dim != 128
+    # decode covers head_dim 64 / 128 / 256 and any group size
+    for good in (ia.decode_desc(32, 8, 64, 4096), ia.decode_desc(16, 8, 256, 4096),
+                 ia.decode_desc(40, 8, 128, 4096), ia.decode_desc(32, 1, 128, 100)):
+        assert lib.ingot_attn_decode_workspace_size(ctypes.byref(good)) > 0
+    for bad in (ia.decode_desc(24, 8, 96, 4096),   # head_dim without a kernel
                 ia.decode_desc(24, 7, 128, 4096),  # not divisible
-                ia.decode_desc(40, 8, 128, 4096),  # group 5
+                ia.decode_desc(512, 8, 128, 4096), # more query heads than epoch words
                 ia.decode_desc(24, 8, 128, 0)):    # no keys
         assert lib.ingot_attn_decode_workspace_size(ctypes.byref(bad)) == 0
     # null pointers are rejected before any HIP call
     rc = lib.ingot_attn_decode(None, None, None, None, None, 0, ctypes.byref(ok), None)
     assert rc == -1
     rc = lib.ingot_attn_decode(None, None, None, None, None, 0,
-                               ctypes.byref(ia.decode_desc(24, 8, 64, 10)), None)
+                               ctypes.byref(ia.decode_desc(24, 8, 96, 10)), None)
     assert rc == -2
+    # one split needs no records; more splits need a record per (split, head)
+    one = ia.decode_desc(24, 8, 128, 100)
+    assert lib.ingot_attn_decode_workspace_size(ctypes.byref(one)) == 65536
+    s = ia.decode_splits(ok)
+    assert s > 1 and lib.ingot_attn_decode_workspace_size(ctypes.byref(ok)) == 65536 + 24 * 32 * (128 * 4 + 16)
     p = ia.prefill_desc(24, 8, 128, 3584, 512)
     assert lib.ingot_attn_prefill_workspace_size(ctypes.byref(p)) > 0
     assert 1 <= ia.prefill_splits(p) <= 16
@@ -127,7 +136,9 @@ def test_split_resolution(lib):
     for n_keys in (1, 2, 63, 64, 65, 511, 512, 4096, 8192, 100000):
         for req in (0, 1, 3, 64, 5000):
             s = ia.decode_splits(ia.decode_desc(24, 8, 128, n_keys, n_splits=req))
-            assert 1 <= s <= min(n_keys, 1024)
+            assert 1 <= s <= min(n_keys, 32)
+            s256 = ia.decode_splits(ia.decode_desc(16, 8, 256, n_keys, n_splits=req))
+            assert 1 <= s256 <= min(n_keys, 16)
             per = -(-n_keys // s)
             assert (s - 1) * per < n_keys  # no empty split
 

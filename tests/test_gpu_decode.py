@@ -34,30 +34,31 @@ def _t(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-def _run_decode(dev, q, kb, vb, n_head, n_head_kv, n_keys, kv_offset=0, n_splits=0):
+def _run_decode(dev, q, kb, vb, n_head, n_head_kv, n_keys, kv_offset=0, n_splits=0, hd=HD,
+                workspace=None):
     import torch
     import ingot_attn as ia
 
-    print(f"[decode] n_head={n_head} n_head_kv={n_head_kv} n_keys={n_keys} "
+    print(f"[decode] n_head={n_head} n_head_kv={n_head_kv} hd={hd} n_keys={n_keys} "
           f"kv_offset={kv_offset} n_splits={n_splits}", flush=True)
     qd = _t(q.astype(np.float32), dev)
     kd = _t(kb.view(np.int16), dev)
     vd = _t(vb.view(np.int16), dev)
-    out = torch.full((n_head * HD,), float("nan"), dtype=torch.float32, device=dev)
-    desc = ia.decode_desc(n_head, n_head_kv, HD, n_keys, kv_offset=kv_offset, n_splits=n_splits)
-    ia.attn_decode(qd, kd, vd, out, desc)
+    out = torch.full((n_head * hd,), float("nan"), dtype=torch.float32, device=dev)
+    desc = ia.decode_desc(n_head, n_head_kv, hd, n_keys, kv_offset=kv_offset, n_splits=n_splits)
+    ia.attn_decode(qd, kd, vd, out, desc, workspace=workspace)
     torch.cuda.synchronize()
     return out.cpu().numpy()
 
 
-def _inputs(seed, n_head, n_head_kv, L, kv_scale=1.0, n_ctx=None):
+def _inputs(seed, n_head, n_head_kv, L, kv_scale=1.0, n_ctx=None, hd=HD):
     rng = np.random.Generator(np.random.PCG64(seed))
     n_ctx = L if n_ctx is None else n_ctx
-    q = rng.standard_normal(n_head * HD).astype(np.float32)
-    kb = np.full((n_ctx, n_head_kv * HD), 0x7E00, dtype=np.uint16)  # NaN past n_keys
-    vb = np.full((n_ctx, n_head_kv * HD), 0x7E00, dtype=np.uint16)
-    kb[:L] = (rng.standard_normal((L, n_head_kv * HD)) * kv_scale).astype(np.float16).view(np.uint16)
-    vb[:L] = (rng.standard_normal((L, n_head_kv * HD)) * kv_scale).astype(np.float16).view(np.uint16)
+    q = rng.standard_normal(n_head * hd).astype(np.float32)
+    kb = np.full((n_ctx, n_head_kv * hd), 0x7E00, dtype=np.uint16)  # NaN past n_keys
+    vb = np.full((n_ctx, n_head_kv * hd), 0x7E00, dtype=np.uint16)
+    kb[:L] = (rng.standard_normal((L, n_head_kv * hd)) * kv_scale).astype(np.float16).view(np.uint16)
+    vb[:L] = (rng.standard_normal((L, n_head_kv * hd)) * kv_scale).astype(np.float16).view(np.uint16)
     return q, kb, vb
 
 
@@ -115,12 +116,61 @@ def test_decode_layer_offset(dev, oracle_mod):
 
 
 def test_decode_repeated_calls_reuse_workspace(dev, oracle_mod):
-    # The completion counters must be back at zero after each call.
+    # Split records of earlier calls stay in the workspace; only the current call's tags match.
     for i, L in enumerate((4096, 700, 4096, 65)):
         q, kb, vb = _inputs(300 + i, H, HKV, L)
         got = _run_decode(dev, q, kb, vb, H, HKV, L)
         want = oracle_mod.attn_decode(q, kb, vb, H, HKV, HD, L, threads=8)
         assert_parity(got, want, f"call {i}")
+
+
+@pytest.mark.parametrize("n_head,n_head_kv,hd", [(32, 8, 64), (16, 8, 256), (8, 8, 64), (4, 2, 256)])
+@pytest.mark.parametrize("L", [1, 513, 4097])
+def test_decode_head_dims(dev, oracle_mod, n_head, n_head_kv, hd, L):
+    # Llama-3.2-1B (32 Q / 8 KV, head_dim 64) and a head_dim-256 model; the reference serves
+    # these through its naive kernel (src/metal_backend.mm:373-382, shaders/kernels.metal:639-702).
+    q, kb, vb = _inputs(40 + L + hd, n_head, n_head_kv, L, n_ctx=L + 8, hd=hd)
+    got = _run_decode(dev, q, kb, vb, n_head, n_head_kv, L, hd=hd)
+    want = oracle_mod.attn_decode(q, kb, vb, n_head, n_head_kv, hd, L, threads=8)
+    assert_parity(got, want, f"hd={hd} G={n_head // n_head_kv} L={L}")
+
+
+@pytest.mark.parametrize("n_head,n_head_kv,hd", [(64, 8, 128), (40, 8, 128), (32, 1, 128), (12, 2, 64),
+                                                  (10, 2, 256), (56, 8, 64), (14, 2, 128)])
+def test_decode_large_groups(dev, oracle_mod, n_head, n_head_kv, hd):
+    # Groups above 4 (the reference's flash decode limit, src/metal_backend.mm:339): up to 8
+    # heads share one workgroup, larger groups take several workgroups per KV head.
+    L = 1500
+    q, kb, vb = _inputs(7 * n_head + hd, n_head, n_head_kv, L, hd=hd)
+    got = _run_decode(dev, q, kb, vb, n_head, n_head_kv, L, hd=hd)
+    want = oracle_mod.attn_decode(q, kb, vb, n_head, n_head_kv, hd, L, threads=8)
+    assert_parity(got, want, f"hd={hd} G={n_head // n_head_kv}")
+
+
+@pytest.mark.parametrize("hd", [64, 256])
+@pytest.mark.parametrize("splits", [1, 2, 5, 32])
+def test_decode_split_invariance_head_dims(dev, oracle_mod, hd, splits):
+    L = 1200
+    q, kb, vb = _inputs(500 + hd, 16, 4, L, hd=hd)
+    got = _run_decode(dev, q, kb, vb, 16, 4, L, n_splits=splits, hd=hd)
+    want = oracle_mod.attn_decode(q, kb, vb, 16, 4, hd, L)
+    assert_parity(got, want, f"hd={hd} splits={splits}")
+
+
+def test_decode_epochs_across_many_calls(dev, oracle_mod):
+    # One workspace, 24 calls whose split counts go up and down: a record slot that an earlier
+    # call wrote (with an older tag) must never be taken for the current call's.
+    import ingot_attn as ia
+
+    ws = ia.Workspace(dev)
+    rng = np.random.Generator(np.random.PCG64(2024))
+    for i in range(24):
+        L = int(rng.integers(200, 3000))
+        splits = int(rng.choice([0, 2, 7, 16, 31, 32]))
+        q, kb, vb = _inputs(900 + i, H, HKV, L)
+        got = _run_decode(dev, q, kb, vb, H, HKV, L, n_splits=splits, workspace=ws)
+        want = oracle_mod.attn_decode(q, kb, vb, H, HKV, HD, L, threads=8)
+        assert_parity(got, want, f"call {i} L={L} splits={splits}")
 
 
 def test_decode_closed_forms(dev):
