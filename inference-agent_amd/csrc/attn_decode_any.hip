@@ -28,7 +28,8 @@
 //     in flight while a step is computed.
 //   - The 4 waves merge through LDS; with one slice wave h writes head h's output, else it
 //     stores head h's record: o[HD] as plain floats, then, once those stores are acknowledged,
-//     the (m, l) chunk {m, l, kFlag, kFlag}. A visible flag therefore means a complete record.
+//     the (m, l) chunk {m, kFlag, l, kFlag}. A visible flag therefore means a complete o, and
+//     m and l each share an 8-byte (single-copy atomic) pair with a flag.
 //
 // Mergers (4 waves, one query head; wave w owns dims [w*HD/4, (w+1)*HD/4)): wave 0 polls the
 // (m, l) chunks of all slices, sleeping between polls, and clears their flags once all are set
@@ -50,9 +51,9 @@
 //   A (16 x 32): lane holds A[i][8g + e], e = 0..7;  B (32 x 16): lane holds B[8g + e][i];
 //   D (16 x 16): lane holds D[4g + j][i], j = 0..3.
 //
-// Workspace: the first kCounterBytes are not used by decode; then one region of
+// Workspace: the first kCounterBytes hold the tuned kernel's counters (unused here); then one region of
 // kDecodeHeadRecordBytes per query head holding the records [split][HD/4 + 1 chunks of 16 B]:
-// o[HD] (f32), then {m, l, kFlag, kFlag} — the reference's part[...][130] record (o, m, l;
+// o[HD] (f32), then {m, kFlag, l, kFlag} — the reference's part[...][130] record (o, m, l;
 // AD_STRIDE at shaders/kernels.metal:291). Every flag a call sets is cleared by that call's
 // merger, and o is only read after its slice's flag was seen, so data left by earlier calls (any
 // head_dim or split count) is never taken for the current call's.
@@ -147,7 +148,7 @@ __device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uin
         for (;;) {
             if (!ok) {
                 ml = __builtin_amdgcn_raw_buffer_load_b128(rs, ml_off, 0, kScDevice);
-                ok = ml[2] == kFlag && ml[3] == kFlag;
+                ok = ml[1] == kFlag && ml[3] == kFlag;
             }
             const uint64_t missing = __builtin_amdgcn_ballot_w64(!ok);
             if (missing == 0 || ++spins >= kSpinLimit) break;
@@ -159,7 +160,7 @@ __device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uin
         if (uint32_t(lane) < n_splits)
             __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, ml_off, 0, kScDevice);
         lds_m[lane] = __uint_as_float(ml[0]);
-        lds_l[lane] = __uint_as_float(ml[1]);
+        lds_l[lane] = __uint_as_float(ml[2]);
         if (lane == 0) lds_ok = spins < kSpinLimit;
     }
     __syncthreads();
@@ -195,7 +196,7 @@ __device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uin
         if constexpr (SPI >= 4) a = add_x16(a);
         acc[e] = add_x32(a);
     }
-    const float inv = !lds_ok ? __builtin_nanf("") : (Lt > 0.f ? 1.f / Lt : 0.f);
+    const float inv = !lds_ok ? __uint_as_float(0x7FC00000u) : (Lt > 0.f ? 1.f / Lt : 0.f);
     if (sg == 0) *reinterpret_cast<float4v*>(out + size_t(head) * HD + 4 * chunk) = acc * inv;
 }
 
@@ -418,7 +419,7 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
         // The flag goes out only once o is acknowledged (in L2, or in memory when written
         // through), so a merger that sees it reads a complete o.
         __builtin_amdgcn_s_waitcnt(0);
-        if (lane == 0) store_record(u32x4{__float_as_uint(M), __float_as_uint(L), kFlag, kFlag}, rs, my + HD * 4, near);
+        if (lane == 0) store_record(u32x4{__float_as_uint(M), kFlag, __float_as_uint(L), kFlag}, rs, my + HD * 4, near);
     }
 }
 
