@@ -128,6 +128,18 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
                        void* workspace, size_t workspace_bytes, const IngotAttnPrefillDesc* d,
                        void* stream);
 
+/* Decode without a caller-provided workspace and without any allocation: the library uses a
+ * device-resident scratch array of INGOT_ATTN_NOALLOC_SCRATCH_BYTES per GPU (enough for up to 64
+ * query heads), resolved and zero-filled on the first call on a device (with a fill kernel on
+ * `stream`). This entry point has no counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and errors as ingot_attn_decode, plus INGOT_ATTN_EWORKSPACE when the
+ * call needs more than the scratch holds (more than 64 query heads). Every call on one GPU shares
+ * that GPU's scratch: calls that overlap on one GPU race, so order them on one stream. */
+#define INGOT_ATTN_NOALLOC_SCRATCH_BYTES (65536u + 64u * 16896u)
+int ingot_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                              float* out, const IngotAttnDecodeDesc* d, void* stream);
+
 /* RoPE and KV-cache store for n_tok tokens at positions pos..pos+n_tok-1, in one launch:
  *   q        [n_tok][q_stride] f32, rotated in place (NULL: only K and V are handled)
  *   k, v     [n_tok][kv_stride] f32 projections

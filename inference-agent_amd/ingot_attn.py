@@ -24,6 +24,7 @@ EXPORTS = (
     "ingot_attn_decode_splits",
     "ingot_attn_prefill_splits",
     "ingot_attn_decode",
+    "ingot_attn_decode_noalloc",
     "ingot_attn_prefill",
     "ingot_rope_kv_store",
     "ingot_attn_strerror",
@@ -151,6 +152,8 @@ def load_library(path: str = LIB_PATH) -> ctypes.CDLL:
     lib.ingot_attn_prefill_splits.restype = c_uint32
     lib.ingot_attn_decode.argtypes = [c_void_p] * 5 + [c_size_t, PD, c_void_p]
     lib.ingot_attn_decode.restype = c_int
+    lib.ingot_attn_decode_noalloc.argtypes = [c_void_p] * 4 + [PD, c_void_p]
+    lib.ingot_attn_decode_noalloc.restype = c_int
     lib.ingot_attn_prefill.argtypes = [c_void_p] * 5 + [c_size_t, PP, c_void_p]
     lib.ingot_attn_prefill.restype = c_int
     lib.ingot_rope_kv_store.argtypes = [c_void_p] * 6 + [ctypes.POINTER(RopeKvDesc), c_void_p]
@@ -262,6 +265,16 @@ def attn_decode(q, k_cache, v_cache, out, desc: DecodeDesc, stream=None, workspa
         c_void_p(out.data_ptr()), c_void_p(ws.data_ptr()), c_size_t(ws.numel()),
         ctypes.byref(desc), _stream_ptr(stream))
     _check(rc, "ingot_attn_decode")
+    return out
+
+
+def attn_decode_noalloc(q, k_cache, v_cache, out, desc: DecodeDesc, stream=None):
+    """ingot_attn_decode_noalloc: the same decode step on the library's device-resident scratch
+    (no workspace argument, no allocation)."""
+    rc = load_library().ingot_attn_decode_noalloc(
+        c_void_p(q.data_ptr()), c_void_p(k_cache.data_ptr()), c_void_p(v_cache.data_ptr()),
+        c_void_p(out.data_ptr()), ctypes.byref(desc), _stream_ptr(stream))
+    _check(rc, "ingot_attn_decode_noalloc")
     return out
 
 
