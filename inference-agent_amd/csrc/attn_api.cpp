@@ -162,7 +162,8 @@ int ingot_proj(const void* const* w, const float* x, const float* norm_w, float*
                                        int(d->prologue), int(d->epilogue), d->eps,
                                        static_cast<hipStream_t>(stream), nullptr,
                                        d->n_tok > 1 ? d->n_tok : 1u);
-    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
+         : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
 
 int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w, float* q, float* k,
@@ -196,7 +197,8 @@ int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w
             lrc = ingot::launch_rope_kv_store(q, k, v, kc, vc, inv_freq, r->n_head, r->n_head_kv,
                                               r->head_dim, r->pos, 1, uint32_t(qd), uint32_t(kvd), st);
     }
-    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
+         : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
 
 uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
@@ -261,7 +263,8 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
     const int lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride,
                                           d->n_head_kv, d->n_head / d->n_head_kv, splits, d->scale,
                                           static_cast<hipStream_t>(stream));
-    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED : INGOT_ATTN_EHIP;
+    return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
+         : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
 
 int ingot_rmsnorm(const float* x, const float* w, float* out, uint32_t n, uint32_t n_rows, float eps,
@@ -327,6 +330,6 @@ const char* ingot_attn_strerror(int code) {
     }
 }
 
-const char* ingot_attn_version(void) { return "ingot-attn-gfx950 0.1"; }
+const char* ingot_attn_version(void) { return "ingot-attn-gfx950 0.2"; }
 
 }  // extern "C"

@@ -403,7 +403,7 @@ template <> struct Col<kBF16> { static constexpr int ndw = 16, bytes = 64; };
 // Q6_K: column c is the 32-element group (h, g) = ((c % 8) / 4, c % 4) of 210-byte block c / 8;
 // the lane loads the windows of its 32 low-bit bytes, its 32 high-bit bytes, its two scales and
 // the block's d.
-template <> struct Col<kQ6_K> { static constexpr int ndw = 20, bytes = 0; };
+template <> struct Col<kQ6_K> { static constexpr int ndw = 20; };
 
 template <int T>
 constexpr bool kStreamed = T == kQ4_0 || T == kQ4_1 || T == kQ8_0 || T == kF16 || T == kBF16 || T == kQ6_K;
@@ -1307,6 +1307,10 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                 const float4v v = {acc[i][4 * q], acc[i][4 * q + 1], acc[i][4 * q + 2], acc[i][4 * q + 3]};
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), prs, off(split, i, q), 0, kScDevice);
             }
+        // The partial's device-scope (write-through) stores are acknowledged by memory before the
+        // arrival is counted, and the last split reads the partials with device-scope loads, which
+        // do not take a clean L2 line: the hand-off needs no release/acquire pair, whose L2
+        // writeback and invalidate around the atomic would cost more than the whole tail.
         __builtin_amdgcn_s_waitcnt(0);  // the partial has reached device scope
         __syncthreads();
         __shared__ unsigned int last;

@@ -59,6 +59,10 @@ struct HostModel {
 
 class HipBackend {
 public:
+    // Tiles (256 rows x 64 tokens, over q, k and v) from which a chunk's q/k/v run as one batched
+    // launch instead of three split-K launches; a test sets 0 to force the one-launch path.
+    uint32_t qkv_one_launch_min_tiles = 128;
+
     // device_weights: the matrices' `data` are device addresses already (gguf::DeviceWeights);
     // otherwise they are host bytes and are copied to the device here.
     HipBackend(const HostModel& m, int n_ctx, int n_batch, hipStream_t stream = nullptr,
@@ -250,9 +254,9 @@ private:
     // A chunk's q/k/v run as one batched launch (no split-K) rather than three split-K
     // ingot_linear calls when the three matrices' tiles of 256 rows x 64 tokens reach half the
     // CUs together (Llama-3.2-3B at 512 tokens: 160 tiles; at 256 tokens 80).
-    static bool qkv_one_launch(uint32_t n_tok, uint32_t q_dim, uint32_t kv_dim) {
+    bool qkv_one_launch(uint32_t n_tok, uint32_t q_dim, uint32_t kv_dim) const {
         const uint32_t rows = (q_dim + 255) / 256 + 2 * ((kv_dim + 255) / 256);
-        return uint64_t(rows) * ((n_tok + 63) / 64) >= 128;
+        return uint64_t(rows) * ((n_tok + 63) / 64) >= qkv_one_launch_min_tiles;
     }
     // One token (or a chunk of n_tok) through 1..3 matrices sharing x (ingot_proj).
     void proj(const Dev* const* w, uint32_t n_mats, const float* x, const float* norm_w, float* const* outs,

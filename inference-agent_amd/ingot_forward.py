@@ -22,13 +22,18 @@ import numpy as np
 import ingot_attn as ia
 
 
+# Tiles (256 rows x 64 tokens over q, k and v) from which a chunk's q/k/v run as one batched
+# launch; a test sets 0 to force that path.
+QKV_ONE_LAUNCH_MIN_TILES = 128
+
+
 def qkv_one_launch(n_tok, q_dim, kv_dim):
     """Whether a chunk's q/k/v run as one batched launch (ingot_proj, no split-K) rather than
     three ingot_linear calls (each split-K over the 256 CUs): when the three matrices' tiles of
     256 rows x 64 tokens reach half the CUs together (Llama-3.2-3B at 512 tokens: 160 tiles; at
     256 tokens 80, where three split launches are faster)."""
     rows = -(-q_dim // 256) + 2 * -(-kv_dim // 256)
-    return rows * -(-n_tok // 64) >= 128
+    return rows * -(-n_tok // 64) >= QKV_ONE_LAUNCH_MIN_TILES
 
 
 class HipForward:

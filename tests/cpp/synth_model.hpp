@@ -76,7 +76,9 @@ struct Owned {
 
 // A two-layer model (512 wide, 4 Q / 2 KV heads of 128, FFN 1024, 500 tokens) with mixed
 // types and tied Q8_0 embeddings.
-inline ingot::HostModel make_model(Owned& own, unsigned seed) {
+// uniform_qkv: wq, wk and wv all Q4_0 (one batched q/k/v launch is possible); otherwise three
+// different types.
+inline ingot::HostModel make_model(Owned& own, unsigned seed, bool uniform_qkv = false) {
     ingot::HostModel m;
     m.n_layer = 2; m.n_embd = 512; m.n_head = 4; m.n_head_kv = 2; m.head_dim = 128;
     m.n_ff = 1024; m.n_vocab = 500; m.rms_eps = 1e-5f;
@@ -98,8 +100,8 @@ inline ingot::HostModel make_model(Owned& own, unsigned seed) {
         for (float& v : L.ffn_norm) v = 1.f + nd(rng);
         const float s = 1.f / std::sqrt(float(m.n_embd));
         L.wq = own.make(2, qd, m.n_embd, s, rng);
-        L.wk = own.make(1, kvd, m.n_embd, s, rng);
-        L.wv = own.make(8, kvd, m.n_embd, s, rng);
+        L.wk = own.make(uniform_qkv ? 2 : 1, kvd, m.n_embd, s, rng);
+        L.wv = own.make(uniform_qkv ? 2 : 8, kvd, m.n_embd, s, rng);
         L.wo = own.make(2, m.n_embd, qd, 0.5f / std::sqrt(float(qd)), rng);
         L.w_gate = own.make(8, m.n_ff, m.n_embd, s, rng);
         L.w_up = own.make(1, m.n_ff, m.n_embd, s, rng);

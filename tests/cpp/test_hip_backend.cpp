@@ -109,6 +109,38 @@ int main() {
             const int32_t bad[2] = {1, m.n_vocab};
             expect(throws([&] { b.forward_batch(bad, 2, 0); }, "token id out of range"), "token id error");
         }
+        {   // wq, wk, wv of one type and the one-launch q/k/v path forced: a chunk, then decode steps
+            synth::Owned own2;
+            const ingot::HostModel m2 = synth::make_model(own2, 12, true);
+            std::vector<OracleLayer> ol2;
+            for (const ingot::HostLayer& L : m2.layers) {
+                auto t = [](const ingot::HostTensor& x) { return OracleTensor{int(x.type), x.data}; };
+                ol2.push_back(OracleLayer{L.attn_norm.data(), L.ffn_norm.data(), t(L.wq), t(L.wk), t(L.wv), t(L.wo),
+                                          t(L.w_gate), t(L.w_up), t(L.w_down)});
+            }
+            OracleModel om2{m2.n_layer, m2.n_embd, m2.n_head, m2.n_head_kv, m2.head_dim, m2.n_ff, m2.n_vocab,
+                            m2.rms_eps, m2.rope_inv_freq.data(), OracleTensor{8, m2.tok_embd.data},
+                            OracleTensor{8, m2.output.data}, m2.output_norm.data(), ol2.data()};
+            std::fill(kc.begin(), kc.end(), 0);
+            std::fill(vc.begin(), vc.end(), 0);
+            ingot::HipBackend b(m2, n_ctx, 48);
+            b.qkv_one_launch_min_tiles = 0;
+            const int n = 40;
+            const float* got = b.forward_batch(toks.data(), n, 0);
+            for (int p = 0; p < n; p++)
+                oracle_forward(&om2, kc.data(), vc.data(), n_ctx, toks[size_t(p)], p, want.data(), 1, 8);
+            double r = rel_l2(got, want.data(), m2.n_vocab);
+            char buf[96];
+            std::snprintf(buf, sizeof buf, "one-launch q/k/v prefill 40 tokens: rel-L2 %.3e", r);
+            expect(r <= 5e-3, buf);
+            for (int p = n; p < n + 3; p++) {
+                got = b.forward(toks[size_t(p)], p);
+                oracle_forward(&om2, kc.data(), vc.data(), n_ctx, toks[size_t(p)], p, want.data(), 0, 8);
+                r = rel_l2(got, want.data(), m2.n_vocab);
+                std::snprintf(buf, sizeof buf, "one-launch q/k/v, decode pos %d: rel-L2 %.3e", p, r);
+                expect(r <= 5e-3, buf);
+            }
+        }
     } catch (const std::exception& e) {
         std::printf("FAIL exception: %s\n", e.what());
         return 1;

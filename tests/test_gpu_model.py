@@ -151,6 +151,23 @@ def test_forward_prefill_then_decode(dev, oracle_mod, types, prefill):
     assert np.linalg.norm(a - b) / np.linalg.norm(b) <= 1e-2
 
 
+@pytest.mark.parametrize("types", ["F16", "Q4_0"])
+def test_forward_prefill_one_launch_qkv(dev, oracle_mod, monkeypatch, types):
+    """The chunk's q/k/v through one batched ingot_proj launch (forced; the real threshold needs
+    a Llama-3.2-3B-sized chunk): logits, the K cache rows it wrote and the decode steps after it
+    against the oracle forward."""
+    import ingot_forward
+
+    monkeypatch.setattr(ingot_forward, "QKV_ONE_LAUNCH_MIN_TILES", 0)
+    res, kc_gpu, kc_orc = _run(dev, oracle_mod, types, prefill=45, decode_steps=3, tied=True)
+    for what, g, w in res:
+        assert np.all(np.isfinite(g))
+        assert _rel(g, w) <= 5e-3, (what, _rel(g, w))
+    a = kc_gpu.view(np.float16).astype(np.float64)
+    b = kc_orc.view(np.float16).astype(np.float64)
+    assert np.linalg.norm(a - b) / np.linalg.norm(b) <= 1e-2
+
+
 def test_forward_errors(dev):
     from ingot_forward import HipForward
 
