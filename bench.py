@@ -13,8 +13,9 @@ divides the algorithmic bytes of one launch by the average launch duration over 
 region (28 x steps launches back to back); the rocprofv3 kernel-trace summary of
 `python bench.py --only c3 --no-cpu` (profiles/attn_decode_C3_kernel_trace.md) gives the same
 kernel's average duration. `roofline.traffic` is the HBM bytes per launch measured with
-rocprofv3 FETCH_SIZE / WRITE_SIZE, calibrated on a copy kernel of known size
-(profiles/attn_decode_C3_traffic.md).
+rocprofv3 FETCH_SIZE / WRITE_SIZE on that kernel, calibrated on a copy kernel of known size
+(`python bench.py --only copy-probe`, profiles/attn_decode_C3_traffic.md); the line names the
+profile and kernel it came from (`traffic_source`).
 
 The same line carries the prefill figures (C4, C5-prefill, C2: TFLOPS and fractions of the
 f16-MFMA and HBM peaks), the decode sweep (C1, C5 lengths), the fused RoPE + KV-cache store
@@ -40,6 +41,8 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
 # HBM bytes per C3 decode launch: (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) KiB from rocprofv3, the
 # factors from the copy probe (profiles/attn_decode_C3_traffic.md).
 C3_TRAFFIC_BYTES = int((8465.0 * 2.0 + 456.75) * 1024)
+C3_TRAFFIC_SOURCE = ("profiles/attn_decode_C3_traffic.md: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 "
+                     "of attn_decode_kernel<3,4> (inference-agent_amd/csrc/attn_decode.hip)")
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 MFMA, 2.5 PFLOP/s
 WARMUP_SECONDS = 0.3
 METRIC = "decode-attn HBM GB/s + prefill-attn TFLOPS, Llama-3.2-3B GQA, 1 MI355X"
@@ -69,7 +72,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    help="all | decode | prefill | kvstore | linear | model | probes | one of "
+                    help="all | decode | prefill | kvstore | linear | model | probes | copy-probe | one of "
                     + ", ".join(list(DECODE) + list(PREFILL) + list(KVSTORE) + list(LINEAR)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -247,6 +250,12 @@ def cpu_baseline(W, seconds):
     import oracle_lib
 
     threads = max(1, min(24, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)), os.cpu_count() or 1))
+    try:
+        import psutil
+
+        physical, logical = psutil.cpu_count(logical=False), psutil.cpu_count()
+    except ImportError:
+        physical, logical = None, os.cpu_count()
     w = W.C3
     q, kb, vb = W.make_inputs(w)
 
@@ -263,6 +272,9 @@ def cpu_baseline(W, seconds):
     dt1 = statistics.median([call(1) for _ in range(5)])
     gbs = lambda t: round(w.decode_bytes() / t / 1e9, 3)
     return {"value": gbs(dt), "unit": "GB/s", "cores": threads, "kind": "port",
+            "host": {"threads_used": threads, "physical_cores": physical, "logical_cpus": logical,
+                     "note": "threads = the box's CPU share for this job (OMP_NUM_THREADS), on a host "
+                             "with the physical cores listed"},
             "single_thread": {"value": gbs(dt1), "ms_per_call": round(dt1 * 1e3, 2)},
             "sample": f"median of {len(times)} oracle decode calls at KV 4096 (C3 shape, one layer slice), "
                       f"{dt * 1e3:.2f} ms/call, {threads} threads over the 24 heads; one thread: median of "
@@ -289,6 +301,18 @@ def probes(torch, W):
     del buf
     out = {"read_C3_bytes": {"us_per_call": round(rd * 1e6, 3), "GB/s": round(n / rd / 1e9, 1),
                              "bytes": n, "frac_of_8TBs": round(n / rd / 8e12, 4)}}
+    # The asymptotic rate: one launch reading 33.6 MB (C5-8192's bytes) and one reading 1 GiB.
+    for name, nbytes, copies, blocks in (("read_C5_8192_bytes", W.Workload("d", "decode", 8192).decode_bytes(), 14, 2048),
+                                         ("read_1GiB", 1 << 30, 2, 8192)):
+        nb = nbytes // 256 * 256
+        big = torch.ones(copies, nb // 4, device=dev)
+        t = time_steps(torch, lambda: [lib.ingot_probe_read(ctypes.c_void_p(big[i].data_ptr()), nb, blocks,
+                                                            ctypes.c_void_p(sink.data_ptr()), stream())
+                                       for i in range(copies)], 10, 2, True) / copies
+        out[name] = {"us_per_call": round(t * 1e6, 2), "GB/s": round(nb / t / 1e9, 1), "bytes": nb,
+                     "workgroups": blocks, "frac_of_8TBs": round(nb / t / 8e12, 4)}
+        del big
+        torch.cuda.empty_cache()
     blocks, iters = 1024, 1000
     for shape, name, mnk in ((0, "mfma_32x32x16_f16", 8 * 32 * 32 * 16), (1, "mfma_16x16x32_f16", 16 * 16 * 16 * 32)):
         t = time_steps(torch, lambda: lib.ingot_probe_mfma(shape, blocks, iters, ctypes.c_void_p(sink.data_ptr()),
@@ -296,6 +320,28 @@ def probes(torch, W):
         flops = blocks * 4 * iters * mnk * 2
         out[name] = {"TFLOPS": round(flops / t / 1e12, 1), "frac_of_2.5PF": round(flops / t / 2.5e15, 4)}
     return out
+
+
+def copy_probe(torch, mib=64):
+    """The plain copy probe (probe_copy) over a buffer of known size, 5 dispatches: the run that
+    calibrates rocprofv3's FETCH_SIZE / WRITE_SIZE against bytes actually moved
+    (rocprofv3 --pmc FETCH_SIZE -- python3 bench.py --only copy-probe)."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "inference-agent_amd", "libingot_probe.so"))
+    lib.ingot_probe_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_void_p]
+    n = mib << 20
+    src = torch.ones(n // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        rc = lib.ingot_probe_copy(ctypes.c_void_p(src.data_ptr()), ctypes.c_void_p(dst.data_ptr()), n, 2048,
+                                  ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError("ingot_probe_copy failed")
+    torch.cuda.synchronize()
+    if not bool((dst == 1).all()):
+        raise RuntimeError("copy probe: wrong result")
+    return {"copy_probe": {"MiB_per_dispatch": mib, "dispatches": 5}}
 
 
 def main():
@@ -316,6 +362,9 @@ def main():
     ia.load_library()
     use_graph = not args.no_graph
     sel = args.only
+    if sel == "copy-probe":
+        print(json.dumps({"metric": METRIC, "results": copy_probe(torch)}), flush=True)
+        return
     want = lambda key, group: sel in ("all", group, key)
     res = {"decode": {}, "prefill": {}, "kv_store": {}, "linear": {}, "model": {}}
 
@@ -416,7 +465,8 @@ def main():
         value, unit, ms = gbs, "GB/s", sps * 1e3
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                    "traffic": C3_TRAFFIC_BYTES, "kernel": "attn_decode_kernel<3,4>",
+                    "traffic": C3_TRAFFIC_BYTES, "traffic_source": C3_TRAFFIC_SOURCE,
+                    "kernel": "attn_decode_kernel<3,4>",
                     "bytes_per_launch": nbytes, "us_per_launch": round(us_thru, 3)}
         workload = ("C3 decode attention, KV 4096, 24 Q / 8 KV heads, hd 128, f16 cache, "
                     "28-layer slice rotation (470 MB)")
