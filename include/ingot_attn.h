@@ -26,11 +26,13 @@
  *   - Not thread-safe per workspace: two calls that share a workspace must be ordered on one
  *     stream.
  *
- * Supported shapes: decode takes head_dim 64, 128 or 256 and any group size n_head / n_head_kv
- * (the reference's flash decode covers head_dim 128 with groups up to 4, src/metal_backend.mm:339,
- * and its naive kernel everything else, src/metal_backend.mm:373-382); head_dim 128 with groups
- * 1..4 runs the tuned kernel. Prefill takes head_dim 128 and groups 1..4. At most 256 query heads
- * (one workspace counter each). Llama-3.2-3B is 24 Q heads / 8 KV heads (group 3).
+ * Supported shapes: head_dim 64, 128 or 256 and any group size n_head / n_head_kv, for decode
+ * and prefill (the reference's flash kernels cover head_dim 128 — decode with groups up to 4,
+ * src/metal_backend.mm:339, prefill any group, :360 — and its naive kernel every other shape,
+ * src/metal_backend.mm:373-382). head_dim 128 runs the tuned kernels (decode groups 1..4 on
+ * attn_decode.hip, prefill on the MFMA kernel in units of up to 4 heads); the other shapes run the
+ * generic kernel. At most 256 query heads (one workspace counter each). Llama-3.2-3B is 24 Q heads /
+ * 8 KV heads (group 3); Llama-3.2-1B 32 / 8 with head_dim 64.
  */
 #ifndef INGOT_ATTN_H
 #define INGOT_ATTN_H
@@ -44,8 +46,7 @@ extern "C" {
 
 #define INGOT_ATTN_OK 0
 #define INGOT_ATTN_EINVAL (-1)      /* null pointer, zero size, pos/n out of range */
-#define INGOT_ATTN_EUNSUPPORTED (-2) /* decode head_dim not 64/128/256; prefill head_dim != 128 or
-                                       group size outside 1..4; n_head > 256;
+#define INGOT_ATTN_EUNSUPPORTED (-2) /* head_dim not 64/128/256; n_head > 256;
                                        linear: weight type or n_in the kernels do not cover */
 #define INGOT_ATTN_EWORKSPACE (-3)  /* workspace smaller than *_workspace_size() */
 #define INGOT_ATTN_EHIP (-4)        /* a HIP runtime call or launch failed */

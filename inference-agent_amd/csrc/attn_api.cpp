@@ -30,16 +30,6 @@ int check_heads(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
     return INGOT_ATTN_OK;
 }
 
-// Prefill: head_dim 128 and n_head / n_head_kv in 1..4 (the MFMA prefill kernel's envelope).
-int check_common(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
-    const int rc = check_heads(n_head, n_head_kv, head_dim);
-    if (rc) return rc;
-    if (head_dim != 128) return INGOT_ATTN_EUNSUPPORTED;
-    const uint32_t group = n_head / n_head_kv;
-    if (group < 1 || group > 4) return INGOT_ATTN_EUNSUPPORTED;
-    return INGOT_ATTN_OK;
-}
-
 // Decode: head_dim 64, 128 or 256, any group size.
 int check_decode(const IngotAttnDecodeDesc* d) {
     if (!d) return INGOT_ATTN_EINVAL;
@@ -51,10 +41,12 @@ int check_decode(const IngotAttnDecodeDesc* d) {
     return INGOT_ATTN_OK;
 }
 
+// Prefill: head_dim 64, 128 or 256, any group size (head_dim 128 on the MFMA kernel).
 int check_prefill(const IngotAttnPrefillDesc* d) {
     if (!d) return INGOT_ATTN_EINVAL;
-    const int rc = check_common(d->n_head, d->n_head_kv, d->head_dim);
+    const int rc = check_heads(d->n_head, d->n_head_kv, d->head_dim);
     if (rc) return rc;
+    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return INGOT_ATTN_EUNSUPPORTED;
     if (d->n_tok == 0 || d->kv_offset % 8 != 0) return INGOT_ATTN_EINVAL;
     if (uint64_t(d->pos) + d->n_tok > 0xffffffffull) return INGOT_ATTN_EINVAL;
     if (d->q_stride < d->n_head * d->head_dim || d->q_stride % 4 != 0) return INGOT_ATTN_EINVAL;
@@ -206,9 +198,18 @@ uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
     return ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
 }
 
+// Prefill split count: the MFMA kernel's (head_dim 128) over its workgroup units; the other head
+// sizes run unsplit.
+uint32_t prefill_split_count(const IngotAttnPrefillDesc* d) {
+    if (d->head_dim != 128) return 1;
+    const uint32_t group = d->n_head / d->n_head_kv;
+    const uint32_t units = d->n_head_kv * (group / ingot::prefill_unit_heads(group));
+    return ingot::prefill_splits(d->pos, d->n_tok, units, d->n_splits);
+}
+
 uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
     if (check_prefill(d)) return 0;
-    return ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
+    return prefill_split_count(d);
 }
 
 size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
@@ -219,7 +220,7 @@ size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
 
 size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d) {
     if (check_prefill(d)) return 0;
-    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
+    const uint32_t splits = prefill_split_count(d);
     const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head * kPartFloats * sizeof(float) : 0;
     // The prefill records follow the decode record regions of the same heads, so a workspace
     // shared by decode and prefill calls never holds prefill data where decode tags are read.
@@ -256,13 +257,19 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
         !aligned16(workspace))
         return INGOT_ATTN_EINVAL;
     if (workspace_bytes < ingot_attn_prefill_workspace_size(d)) return INGOT_ATTN_EWORKSPACE;
-    const uint32_t splits = ingot::prefill_splits(d->pos, d->n_tok, d->n_head_kv, d->n_splits);
-    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_part_offset(d->n_head));
     const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
-    const int lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride,
-                                          d->n_head_kv, d->n_head / d->n_head_kv, splits, d->scale,
-                                          static_cast<hipStream_t>(stream));
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    int lrc;
+    if (d->head_dim == 128) {
+        const uint32_t splits = prefill_split_count(d);
+        auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_part_offset(d->n_head));
+        lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
+                                    d->n_head / d->n_head_kv, splits, d->scale, st);
+    } else {
+        lrc = ingot::launch_prefill_any(q, k, v, out, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
+                                        d->n_head / d->n_head_kv, d->head_dim, d->scale, st);
+    }
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
          : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
@@ -323,7 +330,7 @@ const char* ingot_attn_strerror(int code) {
     switch (code) {
         case INGOT_ATTN_OK: return "ok";
         case INGOT_ATTN_EINVAL: return "invalid argument (null/misaligned pointer, zero size or position out of range)";
-        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (decode: head_dim 64/128/256; prefill: head_dim 128 and n_head/n_head_kv in 1..4; n_head <= 256; linear: weight type without a kernel or n_in not a multiple of its block)";
+        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (attention: head_dim 64/128/256, n_head <= 256; linear: weight type without a kernel or n_in not a multiple of its block)";
         case INGOT_ATTN_EWORKSPACE: return "workspace smaller than the *_workspace_size() figure";
         case INGOT_ATTN_EHIP: return "HIP launch failed";
         default: return "unknown error";

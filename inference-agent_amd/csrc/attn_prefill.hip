@@ -550,6 +550,12 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
 
 }  // namespace
 
+uint32_t prefill_unit_heads(uint32_t group) {
+    for (uint32_t g = group < 4 ? group : 4; g > 1; g--)
+        if (group % g == 0) return g;
+    return 1;
+}
+
 uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t requested) {
     const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
     const uint32_t cap = min(max_tiles, kMaxPrefillSplits);
@@ -595,11 +601,14 @@ int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* 
     if (group > 1 && n_splits == 1 && uint64_t(blocks) * n_head_kv * group <= 256)
         return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv * group, group,
                                    1, qscale, stream);
-    switch (group) {
-        case 1: return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
-        case 2: return launch_prefill_g<2>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
-        case 3: return launch_prefill_g<3>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
-        case 4: return launch_prefill_g<4>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, 1, n_splits, qscale, stream);
+    // Groups above 4 run as units of gs heads (the largest divisor of the group up to 4), kv_div of
+    // them per KV head, each reading that head's K/V.
+    const uint32_t gs = prefill_unit_heads(group), kv_div = group / gs, units = n_head_kv * kv_div;
+    switch (gs) {
+        case 1: return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        case 2: return launch_prefill_g<2>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        case 3: return launch_prefill_g<3>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        case 4: return launch_prefill_g<4>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
         default: return -2;
     }
 }

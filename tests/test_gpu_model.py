@@ -101,16 +101,16 @@ def test_get_rows(dev, oracle_mod, t):
     assert np.all(got[5:] == 0.0)
 
 
-def _run(dev, oracle_mod, types, prefill, decode_steps, tied):
+def _run(dev, oracle_mod, types, prefill, decode_steps, tied, cfg=CFG):
     import torch
     from ingot_forward import HipForward
 
-    m = ls.make_model(CFG, types, seed=7, tied=tied)
+    m = ls.make_model(cfg, types, seed=7, tied=tied)
     n_ctx = 128
     gpu = HipForward(m, n_ctx=n_ctx, n_batch=64, device=dev)
     orc = oracle_mod.ForwardOracle(m, n_ctx=n_ctx)
     rng = np.random.default_rng(8)
-    toks = rng.integers(0, CFG["n_vocab"], prefill + decode_steps).tolist()
+    toks = rng.integers(0, cfg["n_vocab"], prefill + decode_steps).tolist()
     res = []
     g = gpu.forward_batch(toks[:prefill], 0).cpu().numpy()
     want = None
@@ -118,8 +118,8 @@ def _run(dev, oracle_mod, types, prefill, decode_steps, tied):
         want = orc.forward(toks[p], p, f16_linear=prefill > 1)
     res.append(("prefill", g, want))
     # cache rows written by the chunk
-    kv = CFG["n_head_kv"] * CFG["head_dim"]
-    kc = gpu.k_cache.view(torch.int16).cpu().numpy().view(np.uint16).reshape(CFG["n_layer"], n_ctx, kv)
+    kv = cfg["n_head_kv"] * cfg["head_dim"]
+    kc = gpu.k_cache.view(torch.int16).cpu().numpy().view(np.uint16).reshape(cfg["n_layer"], n_ctx, kv)
     for p in range(decode_steps):
         pos = prefill + p
         g = gpu.forward(toks[pos], pos).cpu().numpy()
@@ -160,6 +160,20 @@ def test_forward_prefill_one_launch_qkv(dev, oracle_mod, monkeypatch, types):
 
     monkeypatch.setattr(ingot_forward, "QKV_ONE_LAUNCH_MIN_TILES", 0)
     res, kc_gpu, kc_orc = _run(dev, oracle_mod, types, prefill=45, decode_steps=3, tied=True)
+    for what, g, w in res:
+        assert np.all(np.isfinite(g))
+        assert _rel(g, w) <= 5e-3, (what, _rel(g, w))
+    a = kc_gpu.view(np.float16).astype(np.float64)
+    b = kc_orc.view(np.float16).astype(np.float64)
+    assert np.linalg.norm(a - b) / np.linalg.norm(b) <= 1e-2
+
+
+@pytest.mark.parametrize("head_dim,n_head,n_head_kv", [(64, 8, 2), (256, 4, 2), (128, 8, 1)])
+def test_forward_other_shapes(dev, oracle_mod, head_dim, n_head, n_head_kv):
+    """The whole forward with head_dim 64 (Llama-3.2-1B's; group 4) and 256, and a group of 8
+    (prefill on the MFMA kernel in units of 4 heads): a chunk, then decode steps."""
+    cfg = dict(CFG, n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim)
+    res, kc_gpu, kc_orc = _run(dev, oracle_mod, "F16", prefill=33, decode_steps=3, tied=True, cfg=cfg)
     for what, g, w in res:
         assert np.all(np.isfinite(g))
         assert _rel(g, w) <= 5e-3, (what, _rel(g, w))

@@ -161,3 +161,42 @@ def test_prefill_rows_equal_decode_steps(dev):
         ia.attn_decode(_t(q[i], dev), kd, vd, out, ia.decode_desc(H, HKV, HD, pos + i + 1))
         torch.cuda.synchronize()
         assert_parity(got[i], out.cpu().numpy(), f"row {i}")
+
+
+@pytest.mark.parametrize("n_head,n_head_kv,hd", [(32, 8, 64), (16, 8, 256), (64, 8, 128), (48, 8, 128),
+                                                  (40, 8, 128), (16, 2, 64)])
+def test_prefill_head_dims_and_groups(dev, oracle_mod, n_head, n_head_kv, hd):
+    # head_dim 64 / 256 (the generic kernel, token by token) and groups above 4 on the MFMA
+    # kernel (units of up to 4 heads): the reference takes these through its flash prefill (any
+    # group, src/metal_backend.mm:360) or its naive kernel (shaders/kernels.metal:639-702).
+    import ingot_attn as ia
+    import torch
+
+    pos, n_tok = 40, 300
+    rng = np.random.Generator(np.random.PCG64(n_head * hd))
+    L = pos + n_tok
+    q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    kb = rng.standard_normal((L, n_head_kv * hd)).astype(np.float16).view(np.uint16)
+    vb = rng.standard_normal((L, n_head_kv * hd)).astype(np.float16).view(np.uint16)
+    print(f"[prefill] n_head={n_head} n_head_kv={n_head_kv} hd={hd} {n_tok}@{pos}", flush=True)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    out = torch.full((n_tok, n_head * hd), float("nan"), device=dev)
+    ia.attn_prefill(t(q), t(kb.view(np.int16)), t(vb.view(np.int16)), out,
+                    ia.prefill_desc(n_head, n_head_kv, hd, pos, n_tok))
+    torch.cuda.synchronize()
+    want = oracle_mod.attn_prefill(q, kb, vb, n_head, n_head_kv, hd, pos, n_tok, threads=8)
+    assert_parity(out.cpu().numpy(), want, f"prefill hd={hd} G={n_head // n_head_kv}")
+
+
+def test_prefill_group8_split(dev, oracle_mod):
+    # G = 8 with the key range split (a long chunk over a long prefix)
+    import ingot_attn as ia
+    import torch
+
+    n_head, n_head_kv, pos, n_tok = 64, 8, 3000, 512
+    d = ia.prefill_desc(n_head, n_head_kv, 128, pos, n_tok)
+    print(f"[prefill] G=8 {n_tok}@{pos} splits={ia.prefill_splits(d)}", flush=True)
+    q, kb, vb = _inputs(88, n_head, n_head_kv, pos, n_tok)
+    got = _run_prefill(dev, q, kb, vb, n_head, n_head_kv, pos, n_tok)
+    want = oracle_mod.attn_prefill(q, kb, vb, n_head, n_head_kv, 128, pos, n_tok, threads=16)
+    assert_parity(got, want, "prefill G=8 split")
