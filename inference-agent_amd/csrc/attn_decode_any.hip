@@ -45,7 +45,11 @@
 // of 8) stores its record with plain stores: the lines stay dirty in that XCD's L2, where the
 // merger's device-scope loads find them (~0.3 us one way; a device-scope load takes a line dirty
 // in its own L2 and fetches any other from memory). A walker anywhere else writes through to
-// memory with device-scope stores, where a merger on any XCD finds them.
+// memory with device-scope stores, where a merger on any XCD finds them. The flag says which
+// (kFlagNear / kFlag): a merger that is not on its expected XCD refuses near records (NaN
+// output) rather than read their o lines from memory. Dirty lines do not outlive a call: the
+// kernel's end-of-dispatch release writes L2 back, so a later call's device-scope loads cannot
+// hit a stale dirty line left by a near walker of an earlier call.
 //
 // MFMA 16x16x32 f16 register layouts (wave64, lane l, i = l%16, g = l/16):
 //   A (16 x 32): lane holds A[i][8g + e], e = 0..7;  B (32 x 16): lane holds B[8g + e][i];
@@ -53,7 +57,7 @@
 //
 // Workspace: the first kCounterBytes hold the tuned kernel's counters (unused here); then one region of
 // kDecodeHeadRecordBytes per query head holding the records [split][HD/4 + 1 chunks of 16 B]:
-// o[HD] (f32), then {m, kFlag, l, kFlag} — the reference's part[...][130] record (o, m, l;
+// o[HD] (f32), then {m, flag, l, flag} — the reference's part[...][130] record (o, m, l;
 // AD_STRIDE at shaders/kernels.metal:291). Every flag a call sets is cleared by that call's
 // merger, and o is only read after its slice's flag was seen, so data left by earlier calls (any
 // head_dim or split count) is never taken for the current call's.
@@ -69,7 +73,8 @@ constexpr int kScDevice = 16;             // buffer cache-policy bits: sc1 = dev
 constexpr int kNW = 4;                    // waves per workgroup
 constexpr int kKW = 16;                   // keys per wave step
 constexpr uint32_t kSpinLimit = 1u << 16; // polls before giving up (~16 ms; a real wait is < 50)
-constexpr unsigned kFlag = 0x7E57AB1Eu;    // record-complete marker (an f32 of ~7e37, never an o)
+constexpr unsigned kFlag = 0x7E57AB1Eu;    // record complete, written through to memory
+constexpr unsigned kFlagNear = 0x7E57AB1Fu;  // record complete, left in the walker's XCD's L2
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
@@ -127,9 +132,14 @@ __device__ __forceinline__ void store_record(u32x4 v, __amdgpu_buffer_rsrc_t rs,
 }
 
 // The merging workgroup of one query head (see the file comment).
+// `near`: this merger runs on the XCD its unit's walkers are expected on. A record marked near
+// lives dirty in that XCD's L2, so only a near merger can read it; a merger elsewhere that sees
+// such a flag (its line was evicted, the o lines need not have been) rejects the call with NaN
+// instead of reading o from memory. Under the hardware's round-robin dispatch walkers and
+// mergers are all near or all far, so this only guards against another dispatch order.
 template <int HD>
 __device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uint32_t head,
-                           uint32_t n_splits, int lane, int wave) {
+                           uint32_t n_splits, bool near, int lane, int wave) {
     constexpr int CPW = HD / 16;     // 16-byte o chunks in a wave's quarter of one record
     constexpr int SPI = 64 / CPW;    // splits per load instruction
     constexpr int MAXS = HD > 128 ? int(kMaxDecodeSplits) / 2 : int(kMaxDecodeSplits);
@@ -142,13 +152,16 @@ __device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uin
         recs + size_t(head) * kDecodeHeadRecordBytes, 0, uint32_t(kDecodeHeadRecordBytes), kBufferFlags);
     if (wave == 0) {
         const int ml_off = int(lane * rec_bytes) + HD * 4;
-        bool ok = uint32_t(lane) >= n_splits;
+        bool ok = uint32_t(lane) >= n_splits, stray = false;
         u32x4 ml = {0u, 0u, 0u, 0u};
         uint32_t spins = 0;
         for (;;) {
             if (!ok) {
                 ml = __builtin_amdgcn_raw_buffer_load_b128(rs, ml_off, 0, kScDevice);
-                ok = ml[1] == kFlag && ml[3] == kFlag;
+                const bool far_flag = ml[1] == kFlag && ml[3] == kFlag;
+                const bool near_flag = ml[1] == kFlagNear && ml[3] == kFlagNear;
+                ok = far_flag || near_flag;
+                stray |= near_flag && !near;
             }
             const uint64_t missing = __builtin_amdgcn_ballot_w64(!ok);
             if (missing == 0 || ++spins >= kSpinLimit) break;
@@ -161,7 +174,8 @@ __device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uin
             __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, ml_off, 0, kScDevice);
         lds_m[lane] = __uint_as_float(ml[0]);
         lds_l[lane] = __uint_as_float(ml[2]);
-        if (lane == 0) lds_ok = spins < kSpinLimit;
+        const bool strays = __builtin_amdgcn_ballot_w64(stray) != 0;
+        if (lane == 0) lds_ok = spins < kSpinLimit && !strays;
     }
     __syncthreads();
     const bool have = uint32_t(lane) < n_splits;
@@ -222,7 +236,8 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
     const uint32_t n_walk = per_tok * n_tok;
     if (blockIdx.x >= n_walk) {  // (several slices only with one token: decode)
         const uint32_t m = blockIdx.x - n_walk, unit = m % n_units, h = m / n_units;
-        merge_head<HD>(recs, out, (unit / n_sub) * group + (unit % n_sub) * G + h, n_splits, lane, wave);
+        const bool near = (n_units & 7) == 0 && xcc_id() == (blockIdx.x & 7);
+        merge_head<HD>(recs, out, (unit / n_sub) * group + (unit % n_sub) * G + h, n_splits, near, lane, wave);
         return;
     }
 
@@ -426,7 +441,8 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
         // The flag goes out only once o is acknowledged (in L2, or in memory when written
         // through), so a merger that sees it reads a complete o.
         __builtin_amdgcn_s_waitcnt(0);
-        if (lane == 0) store_record(u32x4{__float_as_uint(M), kFlag, __float_as_uint(L), kFlag}, rs, my + HD * 4, near);
+        const unsigned flag = near ? kFlagNear : kFlag;
+        if (lane == 0) store_record(u32x4{__float_as_uint(M), flag, __float_as_uint(L), flag}, rs, my + HD * 4, near);
     }
 }
 
