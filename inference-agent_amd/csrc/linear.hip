@@ -1056,6 +1056,10 @@ __device__ __forceinline__ half8 frag(const Raw<T>& r, int s, uint32_t k0) {
 constexpr int kScDevice = 16;                 // buffer cache-policy bits: sc1 = device scope
 constexpr uint32_t kTileFloats = kMmToks * kMmRows;
 constexpr uint32_t kMaxSplits = 8;
+// Output transpose: one 32-token half of a wave's 64 x 32 tile at a time, rows of 32 floats
+// at a pitch of 40 (the two token groups of a write instruction land in opposite bank halves).
+constexpr int kOutPitch = 40;
+constexpr int kOutStage = 32 * kOutPitch;
 
 // W staged through LDS (LW kernels): a stage is `ks` elements of every row of the tile, `bytes`
 // per row (a whole number of 16-byte chunks, so lanes load full cache lines), stored at a row
@@ -1126,6 +1130,10 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     float16v_ acc[2];
     for (int i = 0; i < 2; i++)
         for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
+    // LDS for the output transpose (kOutStage floats per wave): the W buffers once the loop
+    // is done (LW), else an array of its own.
+    __shared__ __attribute__((aligned(16))) float ost_direct[LW ? 4 : kMmWaves * kOutStage];
+    float* ost = ost_direct;
 
     if constexpr (LW) {
         // W and x through LDS, one stage (`ks` elements of k) at a time, one barrier per stage:
@@ -1148,6 +1156,8 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         static_assert(2 * kMmRows * PITCH + 2 * kMmToks * XP * 2 <= 160 * 1024, "LDS");
         __shared__ __attribute__((aligned(16))) _Float16 xst[2][kMmToks * XP];
         extern __shared__ __attribute__((aligned(16))) uint8_t wsm[];  // [2][kMmRows][PITCH]
+        static_assert(kMmWaves * kOutStage * 4 <= 2 * kMmRows * PITCH, "output staging fits");
+        ost = reinterpret_cast<float*>(wsm);
         const uint32_t nst = steps / P;
         const uint32_t rows_here = min(n_out - rtl * kMmRows, uint32_t(kMmRows));
         const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
@@ -1211,6 +1221,9 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                 if (j >= nst) break;
                 const uint8_t* wrow = wsm + jj * (kMmRows * PITCH) + (wave * kMmRowsWave + n) * PITCH;
                 load_w(jj, j + 2);  // this slot's stage j is already in LDS
+                // Issue the prefetch here: left to the scheduler, these loads sink below the
+                // stage's MFMAs and the next stage waits for them.
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (uint32_t xs_i = 0; xs_i < NXS; xs_i++) {
                     const uint32_t xb = (jj * NXS + xs_i) & 1;  // x buffer of x stage j*NXS + xs_i
@@ -1231,6 +1244,9 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                             }
                         }
                     }
+                    // The stage's MFMAs before its LDS writes (hoisted above them, the writes would
+                    // wait for x loads issued just before the previous barrier).
+                    __builtin_amdgcn_sched_barrier(0);
                     store_xs(xb ^ 1);  // x of the next x stage
                     if (xs_i == NXS - 1) store_w(jj ^ 1);  // W of stage j+1
                     load_xs(j * NXS + xs_i + 2);
@@ -1321,34 +1337,67 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         }
         __syncthreads();
         if (!last) return;
-        // Sum the partials in split order; all loads of a partial are issued together and the
-        // next partial's loads are in flight while the current one is added.
+        // Sum the partials in split order (this split's own from registers, the others'
+        // loaded); all loads of a partial are issued together and the next partial's loads are
+        // in flight while the current one is added.
+        float16v_ own[2] = {acc[0], acc[1]};
         for (int i = 0; i < 2; i++)
             for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
         float4v pv[2][8];
         auto load_part = [&](int slot, uint32_t sp) {
+            if (sp == split) return;
             for (int i = 0; i < 2; i++)
                 for (int q = 0; q < 4; q++)
                     pv[slot][i * 4 + q] = __builtin_bit_cast(
                         float4v, __builtin_amdgcn_raw_buffer_load_b128(prs, off(sp, i, q), 0, kScDevice));
         };
+        auto add_part = [&](int slot, uint32_t sp) {
+            for (int i = 0; i < 2; i++)
+                for (int q = 0; q < 4; q++)
+                    for (int e = 0; e < 4; e++)
+                        acc[i][4 * q + e] += sp == split ? own[i][4 * q + e] : pv[slot][i * 4 + q][e];
+        };
         load_part(0, 0);
         for (uint32_t sp = 0; sp < splits; sp += 2) {
-            load_part(1, min(sp + 1, splits - 1));
-            for (int i = 0; i < 2; i++)
-                for (int q = 0; q < 4; q++)
-                    for (int e = 0; e < 4; e++) acc[i][4 * q + e] += pv[0][i * 4 + q][e];
+            if (sp + 1 < splits) load_part(1, sp + 1);
+            add_part(0, sp);
             if (sp + 1 >= splits) break;
-            load_part(0, min(sp + 2, splits - 1));
-            for (int i = 0; i < 2; i++)
-                for (int q = 0; q < 4; q++)
-                    for (int e = 0; e < 4; e++) acc[i][4 * q + e] += pv[1][i * 4 + q][e];
+            if (sp + 2 < splits) load_part(0, sp + 2);
+            add_part(1, sp + 1);
         }
         if (tid == 0)  // leave the workspace ready for the next call
             __hip_atomic_store(counters + tile * 16, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // Output: all previous values are read before any store (the stores could alias later
-    // loads otherwise, which serializes every read-modify-write).
+    // Output: out[tok][row] = prev + acc for the wave's 64 tokens x 32 rows. With 16-byte
+    // aligned rows the tile is transposed through LDS, 32 tokens at a time, so that each lane
+    // loads and stores 16 contiguous bytes (8 lanes per token row: 8 instructions each way
+    // instead of 32 scattered 4-byte ones); all previous values are read before any store.
+    const bool vec = ((reinterpret_cast<uintptr_t>(out) | (size_t(n_out) * 4)) & 15) == 0;
+    if (vec) {
+        const uint32_t tr = lane / 8, c4 = 4 * (lane % 8);  // token row within 8, first row
+        const uint32_t row0 = rowbase + c4;
+        float4v prev[2][4];
+        for (int i = 0; i < 2; i++)
+            for (int k = 0; k < 4; k++) {
+                const uint32_t tok = tok0 + 32 * i + 8 * k + tr;
+                prev[i][k] = accumulate && tok < n_tok && row0 < n_out
+                    ? *reinterpret_cast<const float4v*>(out + size_t(tok) * n_out + row0)
+                    : float4v{0.f, 0.f, 0.f, 0.f};
+            }
+        float* st = ost + wave * kOutStage;
+        for (int i = 0; i < 2; i++) {
+            __syncthreads();  // the staging area is free (loop reads, or the previous half)
+            for (int e = 0; e < 16; e++) st[(8 * (e / 4) + 4 * h + e % 4) * kOutPitch + n] = acc[i][e];
+            __syncthreads();
+            for (int k = 0; k < 4; k++) {
+                const uint32_t tok = tok0 + 32 * i + 8 * k + tr;
+                const float4v v = *reinterpret_cast<const float4v*>(st + (8 * k + tr) * kOutPitch + c4);
+                if (tok < n_tok && row0 < n_out)
+                    *reinterpret_cast<float4v*>(out + size_t(tok) * n_out + row0) = prev[i][k] + v;
+            }
+        }
+        return;
+    }
     const uint32_t orow = rowbase + n;
     if (orow < n_out) {
         float prev[2][16];
