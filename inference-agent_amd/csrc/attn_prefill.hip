@@ -32,6 +32,8 @@
 //   D (16 x 16): lane holds D[4g + j][i], j = 0..3.
 // ds_read_b64_tr_b16 (per 16-lane group; lane r supplies an address, lane i receives 4 halves):
 //   out[i][j] = halves[4j + i/4][i%4], where halves[r][0..3] are the 4 halves at lane r's address.
+#include <type_traits>
+
 #include "attn_common.h"
 #include "attn_internal.h"
 
@@ -74,7 +76,18 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                          const _Float16* __restrict__ V, float* __restrict__ out,
                          float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
                          uint32_t n_head_kv, uint32_t kv_div, uint32_t tps, float qscale) {
-    extern __shared__ __attribute__((aligned(16))) char smem[];
+    // LDS: one object per (key group, buffer) stage, so the compiler can tell that the reads of
+    // the current stage do not touch the stage being filled by the DMA (with one array it waits
+    // for every copy in flight before each transposing read), and the (m, l) fields of the
+    // key-group merge.
+    __shared__ __attribute__((aligned(16))) char sg00[kStageBytes];
+    __shared__ __attribute__((aligned(16))) char sg01[kStageBytes];
+    __shared__ __attribute__((aligned(16))) char sg10[KG > 1 ? kStageBytes : 16];
+    __shared__ __attribute__((aligned(16))) char sg11[KG > 1 ? kStageBytes : 16];
+    __shared__ __attribute__((aligned(16))) float4v mlx[KG > 1 ? G : 1][QW][64];
+    auto stage_of = [&](uint32_t g_, int b) -> char* {
+        return b == 0 ? (g_ != 0 ? sg10 : sg00) : (g_ != 0 ? sg11 : sg01);
+    };
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
@@ -117,7 +130,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     const _Float16* Vg = V + size_t(kvh / kv_div) * kHeadDim;
 
     // Tile copy HBM -> LDS: 32 buffer_load ... lds instructions of 1 KB (4 rows) per tile,
-    // spread over the waves of the key group and issued in four parts between the compute
+    // spread over the waves of the key group and issued in two groups between the compute
     // phases of the current tile, so that the CU's address unit never receives all of them at
     // once (a burst stalls every wave at the issue). Lane l of an instruction fills physical
     // chunk l%16 of row 4*i + l/16, so it fetches the logical chunk (l%16) ^ swizzle(row). The
@@ -125,7 +138,6 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // tile and its size covers only the visible rows, so rows past kend read as zeros (finite;
     // those keys are masked, so their P is exactly 0) with no clamping arithmetic.
     constexpr int kInstPerWave = 32 / QW;  // each key group copies its own tiles
-    constexpr int kInstPerPart = kInstPerWave / 4;
     const uint32_t row_bytes = uint32_t(kv_dim) * 2;
     uint32_t dma_off[kInstPerWave];
 #pragma unroll
@@ -136,21 +148,17 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         const int logical = (lane & 15) ^ (isv ? swz_v(row) : swz_k(row));
         dma_off[k] = uint32_t(row) * row_bytes + 16u * uint32_t(logical);
     }
-    auto issue_part = [&](uint32_t t, int buf, int part_) {
+    // Copy instruction k (0 .. kInstPerWave-1) of this wave for tile t into buffer `buf`.
+    auto issue_inst = [&](uint32_t t, int buf, int k) {
         const uint32_t kb = t * kBN;
-        char* stage = smem + (kg * 2 + buf) * kStageBytes;
+        char* stage = stage_of(kg, buf);
         const uint32_t nrec = min(kend - kb, uint32_t(kBN)) * row_bytes;
-        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<_Float16*>(Kg + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
-        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<_Float16*>(Vg + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
-#pragma unroll
-        for (int k = part_ * kInstPerPart; k < (part_ + 1) * kInstPerPart; k++) {
-            const int i = qw + k * QW;  // wave-uniform
-            const int isv = i >> 4;
-            char* dst = stage + isv * kTileBytes + (4 * (i & 15)) * kRowBytes;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(isv ? rv : rk, (lds_void*)dst, 16, int(dma_off[k]), 0, 0, 0);
-        }
+        const int i = qw + k * QW;  // wave-uniform
+        const int isv = i >> 4;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<_Float16*>((isv ? Vg : Kg) + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
+        char* dst = stage + isv * kTileBytes + (4 * (i & 15)) * kRowBytes;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 16, int(dma_off[k]), 0, 0, 0);
     };
 
     // Q is loaded once per workgroup: every thread converts part of the workgroup's
@@ -181,7 +189,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     uint32_t t_first = t_begin + kg;
     if (t_begin < t_end && t_first < t_end)
 #pragma unroll
-        for (int p = 0; p < 4; p++) issue_part(t_first, 0, p);
+        for (int k = 0; k < kInstPerWave; k++) issue_inst(t_first, 0, k);
 #pragma unroll
     for (int it = 0; it < kQIt; it++) {
         const int idx = tid + it * NT;
@@ -191,7 +199,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         half4 y;
 #pragma unroll
         for (int e = 0; e < 4; e++) y[e] = _Float16(qx[it][e] * qscale);
-        char* qs = smem + ((ql >> 5) * 2 + 1) * kStageBytes;
+        char* qs = stage_of(ql >> 5, 1);
         const int chunk = (c4 >> 1) ^ (ql & 15);
         *reinterpret_cast<half4*>(qs + ((ql & 31) * G + h) * kRowBytes + 16 * chunk + 8 * (c4 & 1)) = y;
     }
@@ -200,7 +208,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     half8 qb[G][4];
     {
         const int ql = 16 * qw + li;
-        const char* qs = smem + ((ql >> 5) * 2 + 1) * kStageBytes + (ql & 31) * G * kRowBytes;
+        const char* qs = stage_of(ql >> 5, 1) + (ql & 31) * G * kRowBytes;
 #pragma unroll
         for (int h = 0; h < G; h++)
 #pragma unroll
@@ -229,14 +237,16 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         for (int d = 0; d < 8; d++) O[h][d] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
-    // `dma(p)` issues part p of the next tile's copy.
-    auto compute_tile = [&](uint32_t t, int buf, auto&& dma) {
+    // `dma(k)` issues copy instruction k of the next tile (k < kInstPerWave).
+    auto compute_tile = [&](uint32_t t, auto bufc, auto&& dma) {
+        constexpr int buf = decltype(bufc)::value;
         const uint32_t kb = t * kBN;
         if (kb >= kend_w) {  // every key of this tile is in this wave's future
-            dma(0); dma(1); dma(2); dma(3);
+#pragma unroll
+            for (int k = 0; k < kInstPerWave; k++) dma(k);
             return;
         }
-        const char* Ks = smem + (kg * 2 + buf) * kStageBytes;
+        const char* Ks = stage_of(kg, buf);
         const char* Vs = Ks + kTileBytes;
 
         // Two halves of 32 keys (scores, online-softmax update, P*V each), so only 32 keys'
@@ -350,27 +360,36 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         // switches break the lockstep of the two waves on a SIMD (which the per-tile barrier
         // restores), so one wave's VALU work lines up more often with the other's matrix work
         // (measured: C5 187.8 -> 182.6 us; which phase gets the priority makes no difference).
-        dma(0);
+        // The next tile's copy goes out in two halves of 4 instructions: after the first P*V
+        // half and after the second half's scores. The compiler waits for every copy in flight
+        // before a transposing LDS read (it cannot tell them apart), so no copy may be issued
+        // before or among the first half's reads; these have the second half's softmax (and
+        // scores) to land before its P*V, and the next tile's start is not held up. (Copies
+        // issued among the P*V reads made C5 1.9x slower; all 8 after the first half measured
+        // like this split within 1%.)
+        static_assert(kInstPerWave == 8, "two groups of 4 copies");
         __builtin_amdgcn_s_setprio(1);
         scores(0);
         __builtin_amdgcn_s_setprio(0);
-        dma(1);
         softmax(0);
         __builtin_amdgcn_s_setprio(1);
         pv(0, P);
         __builtin_amdgcn_s_setprio(0);
-        dma(2);
+#pragma unroll
+        for (int k = 0; k < 4; k++) dma(k);
         if (kb + 32 < kend_w) {
             __builtin_amdgcn_s_setprio(1);
             scores(1);
             __builtin_amdgcn_s_setprio(0);
-            dma(3);
+#pragma unroll
+            for (int k = 4; k < 8; k++) dma(k);
             softmax(1);
             __builtin_amdgcn_s_setprio(1);
             pv(1, P);
             __builtin_amdgcn_s_setprio(0);
         } else {
-            dma(3);
+#pragma unroll
+            for (int k = 4; k < 8; k++) dma(k);
         }
     };
 
@@ -378,51 +397,53 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // (one barrier per step).
     if (t_begin < t_end) {
         const uint32_t steps = (t_end - t_begin + KG - 1) / KG;
-        uint32_t t = t_first;
         __builtin_amdgcn_s_waitcnt(0);  // this wave's Q reads and first-tile copies are done
         __syncthreads();                // ... and everyone's: the Q staging may be overwritten
-        int buf = 0;
-        for (uint32_t st = 0; st < steps; st++, t += KG) {
+        // One step: tile t from buffer `buf` while the next tile of this key group streams into
+        // the other buffer (two steps per iteration, so the buffers are fixed in the code).
+        auto step = [&](uint32_t t, auto bufc) {
+            constexpr int buf = decltype(bufc)::value;
             const bool next = t + KG < t_end;
-            auto dma = [&](int p) {
-                if (next) issue_part(t + KG, buf ^ 1, p);
+            auto dma = [&](int k) {
+                if (next) issue_inst(t + KG, buf ^ 1, k);
             };
-            if (t < t_end) compute_tile(t, buf, dma);
+            if (t < t_end) compute_tile(t, bufc, dma);
             else {
-                dma(0); dma(1); dma(2); dma(3);
+#pragma unroll
+                for (int k = 0; k < kInstPerWave; k++) dma(k);
             }
             __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of the next tile have landed
             __syncthreads();                // ... and everyone's; this tile is no longer read
-            buf ^= 1;
+        };
+        uint32_t t = t_first;
+        for (uint32_t st = 0; st < steps; st += 2, t += 2 * KG) {
+            step(t, std::integral_constant<int, 0>{});
+            if (st + 1 < steps) step(t + KG, std::integral_constant<int, 1>{});
         }
     }
 
     if (KG == 2) {
         // Merge the two key groups through LDS (the tiles are no longer read): group 1 stores
-        // its (O, m, l, started) per lane for as many heads as fit (all 3 for G = 3), one
-        // barrier, group 0 folds them in with the log-sum-exp rule. 9 16-byte fields x 64 lanes
-        // x QW waves per head, lane-minor (conflict-free 16-byte LDS accesses).
-        constexpr int kFields = 9;
-        constexpr int kHR = (KG * 2 * kStageBytes) / (QW * kFields * 64 * 16);  // heads per round
-        static_assert(kHR >= 1, "merge buffer fits");
-#pragma unroll
-        for (int h0 = 0; h0 < G; h0 += kHR) {
-            if (h0 > 0) __syncthreads();  // the previous round's reads are done
+        // its (O, m, l, started) per lane for every head, one barrier, group 0 folds them in
+        // with the log-sum-exp rule. Head h's O goes to stage object h (8 16-byte fields x 64
+        // lanes x QW waves = one stage), its (m, l) to mlx; lane-minor, conflict-free.
+        static_assert(G <= 4 && QW * 8 * 64 * 16 == kStageBytes, "merge buffers");
+        {
             if (kg == 1) {
 #pragma unroll
-                for (int h = h0; h < min(G, h0 + kHR); h++) {
-                    float4v* st = reinterpret_cast<float4v*>(smem) + ((h - h0) * QW + qw) * kFields * 64 + lane;
+                for (int h = 0; h < G; h++) {
+                    float4v* st = reinterpret_cast<float4v*>(stage_of(h >> 1, h & 1)) + qw * 8 * 64 + lane;
 #pragma unroll
                     for (int d = 0; d < 8; d++) st[d * 64] = O[h][d];
-                    st[8 * 64] = float4v{m[h], l[h], started[h] ? 1.f : 0.f, 0.f};
+                    mlx[h][qw][lane] = float4v{m[h], l[h], started[h] ? 1.f : 0.f, 0.f};
                 }
             }
             __syncthreads();
             if (kg == 0) {
 #pragma unroll
-                for (int h = h0; h < min(G, h0 + kHR); h++) {
-                    const float4v* st = reinterpret_cast<const float4v*>(smem) + ((h - h0) * QW + qw) * kFields * 64 + lane;
-                    const float4v ml = st[8 * 64];
+                for (int h = 0; h < G; h++) {
+                    const float4v* st = reinterpret_cast<const float4v*>(stage_of(h >> 1, h & 1)) + qw * 8 * 64 + lane;
+                    const float4v ml = mlx[h][qw][lane];
                     const float m1 = ml[0], l1 = ml[1];
                     const bool s1 = ml[2] != 0.f;
                     const float M = started[h] ? (s1 ? fmaxf(m[h], m1) : m[h]) : m1;
@@ -529,12 +550,7 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
     }
     if (uint64_t(pairs) * n_head_kv > 0x7fffffffu) return -1;
     const dim3 grid(pairs * n_head_kv);
-    const size_t lds = size_t(kKG) * 2 * kStageBytes;  // 128 KB: two double-buffered stages
-    static const hipError_t attr = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&attn_prefill_kernel<G, kQW, kKG>),
-        hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
-    if (attr != hipSuccess) return -4;
-    hipLaunchKernelGGL((attn_prefill_kernel<G, kQW, kKG>), grid, dim3(64 * kQW * kKG), lds, stream,
+    hipLaunchKernelGGL((attn_prefill_kernel<G, kQW, kKG>), grid, dim3(64 * kQW * kKG), 0, stream,
                        q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, kv_div, tps, qscale);
     if (hipGetLastError() != hipSuccess) return -4;
     if (n_splits > 1) {
