@@ -567,7 +567,10 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
 }  // namespace
 
 uint32_t prefill_unit_heads(uint32_t group) {
-    for (uint32_t g = group < 4 ? group : 4; g > 1; g--)
+    // At most 3 heads per unit: the 4-head instantiation needs more than the 256 registers two
+    // waves per SIMD leave and spills (measured 163 TFLOP/s at 32 Q / 8 KV heads, C4 shape,
+    // against 600 for 3 heads), so a group of 4 runs as two units of 2.
+    for (uint32_t g = group < 3 ? group : 3; g > 1; g--)
         if (group % g == 0) return g;
     return 1;
 }
@@ -617,14 +620,13 @@ int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* 
     if (group > 1 && n_splits == 1 && uint64_t(blocks) * n_head_kv * group <= 256)
         return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv * group, group,
                                    1, qscale, stream);
-    // Groups above 4 run as units of gs heads (the largest divisor of the group up to 4), kv_div of
+    // Groups above 3 run as units of gs heads (the largest divisor of the group up to 3), kv_div of
     // them per KV head, each reading that head's K/V.
     const uint32_t gs = prefill_unit_heads(group), kv_div = group / gs, units = n_head_kv * kv_div;
     switch (gs) {
         case 1: return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
         case 2: return launch_prefill_g<2>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
         case 3: return launch_prefill_g<3>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
-        case 4: return launch_prefill_g<4>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
         default: return -2;
     }
 }
