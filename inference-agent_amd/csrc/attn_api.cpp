@@ -198,10 +198,10 @@ uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
     return ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
 }
 
-// Prefill split count: the MFMA kernel's (head_dim 128) over its workgroup units; the other head
-// sizes run unsplit.
+// Prefill split count: the MFMA kernel's (head_dim 64 and 128) over its workgroup units; the
+// other head size runs unsplit.
 uint32_t prefill_split_count(const IngotAttnPrefillDesc* d) {
-    if (d->head_dim != 128) return 1;
+    if (!ingot::prefill_mfma_head_dim(d->head_dim)) return 1;
     const uint32_t group = d->n_head / d->n_head_kv;
     const uint32_t units = d->n_head_kv * (group / ingot::prefill_unit_heads(group));
     return ingot::prefill_splits(d->pos, d->n_tok, units, d->n_splits);
@@ -261,11 +261,11 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     int lrc;
-    if (d->head_dim == 128) {
+    if (ingot::prefill_mfma_head_dim(d->head_dim)) {
         const uint32_t splits = prefill_split_count(d);
         auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_part_offset(d->n_head));
         lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
-                                    d->n_head / d->n_head_kv, splits, d->scale, st);
+                                    d->n_head / d->n_head_kv, d->head_dim, splits, d->scale, st);
     } else {
         lrc = ingot::launch_prefill_any(q, k, v, out, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
                                         d->n_head / d->n_head_kv, d->head_dim, d->scale, st);

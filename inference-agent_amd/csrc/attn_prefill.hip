@@ -50,9 +50,12 @@ typedef __attribute__((address_space(3))) half8 lds_half8;
 constexpr int kBN = 64;                        // keys per tile
 constexpr float kLazy = 8.f;                   // base-2 headroom before the reference max moves
 constexpr int kBufferFlags = 0x00020000;       // buffer descriptor word 3 (raw, 32-bit format)
-constexpr int kRowBytes = kHeadDim * 2;        // 256 B per K/V row in LDS (no padding)
-constexpr int kTileBytes = kBN * kRowBytes;    // 16 KB per K or V tile
-constexpr int kStageBytes = 2 * kTileBytes;    // K + V
+// LDS geometry for head size HD: a K/V row of HD halves (no padding), 16-byte chunks per row,
+// a K or V tile of kBN rows, a stage = K tile + V tile (HD 128: 256 B, 16, 16 KB, 32 KB).
+template <int HD> constexpr int kRowBytes = HD * 2;
+template <int HD> constexpr int kChunks = HD / 8;
+template <int HD> constexpr int kTileBytes = kBN * kRowBytes<HD>;
+template <int HD> constexpr int kStageBytes = 2 * kTileBytes<HD>;
 
 // Max over the 4 lanes l, l^16, l^32, l^48 (the lanes that hold one query column) with the
 // gfx950 lane-swap instructions: with both operands equal to x, the two results of
@@ -66,24 +69,37 @@ __device__ __forceinline__ float max_lanes4(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// XOR swizzles of the 16-byte chunk index (0..15) inside a 256-byte row.
-__device__ __forceinline__ int swz_k(int row) { return row & 15; }       // A-operand row reads
-__device__ __forceinline__ int swz_v(int row) { return (row & 7) << 1; }  // transposing reads
+// XOR swizzles of the 16-byte chunk index inside a row, chosen so that the 16 lanes of a
+// 16-byte K read (16 rows, one logical chunk) and the 32 lanes of a transposing V read (8 rows,
+// a 32-byte chunk pair each) cover all 64 banks once. A 256-byte row spans the 64 banks, so
+// the chunk (pair) index alone must differ; a 128-byte row spans half of them, so rows of the
+// same parity must differ, hence row >> 1.
+template <int HD> __device__ __forceinline__ int swz_k(int row) {
+    return HD == 64 ? (row >> 1) & 7 : row & 15;
+}
+template <int HD> __device__ __forceinline__ int swz_v(int row) {
+    return HD == 64 ? ((row >> 1) & 3) << 1 : (row & 7) << 1;
+}
 
-template <int G, int QW, int KG>
-__global__ __launch_bounds__(64 * QW * KG) __attribute__((amdgpu_waves_per_eu(G == 4 ? 1 : 2)))
+template <int HD, int G, int QW, int KG>
+__global__ __launch_bounds__(64 * QW * KG) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict__ K,
                          const _Float16* __restrict__ V, float* __restrict__ out,
                          float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
                          uint32_t n_head_kv, uint32_t kv_div, uint32_t tps, float qscale) {
+    constexpr int RB = kRowBytes<HD>, CPR = kChunks<HD>, TB = kTileBytes<HD>, SB = kStageBytes<HD>;
+    constexpr int NIT = TB / 1024;  // 1 KB copy instructions per K (or V) tile
+    constexpr int RPI = 1024 / RB;  // rows per copy instruction
+    constexpr int KS = HD / 32;     // 32-wide k steps of a score MFMA chain
+    constexpr int ND = HD / 16;     // 16-dim blocks of O
     // LDS: one object per (key group, buffer) stage, so the compiler can tell that the reads of
     // the current stage do not touch the stage being filled by the DMA (with one array it waits
     // for every copy in flight before each transposing read), and the (m, l) fields of the
     // key-group merge.
-    __shared__ __attribute__((aligned(16))) char sg00[kStageBytes];
-    __shared__ __attribute__((aligned(16))) char sg01[kStageBytes];
-    __shared__ __attribute__((aligned(16))) char sg10[KG > 1 ? kStageBytes : 16];
-    __shared__ __attribute__((aligned(16))) char sg11[KG > 1 ? kStageBytes : 16];
+    __shared__ __attribute__((aligned(16))) char sg00[SB];
+    __shared__ __attribute__((aligned(16))) char sg01[SB];
+    __shared__ __attribute__((aligned(16))) char sg10[KG > 1 ? SB : 16];
+    __shared__ __attribute__((aligned(16))) char sg11[KG > 1 ? SB : 16];
     __shared__ __attribute__((aligned(16))) float4v mlx[KG > 1 ? G : 1][QW][64];
     auto stage_of = [&](uint32_t g_, int b) -> char* {
         return b == 0 ? (g_ != 0 ? sg10 : sg00) : (g_ != 0 ? sg11 : sg01);
@@ -103,7 +119,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // (n_head_kv counts units, kv_div of them per KV head): the group's heads run in separate
     // workgroups, each reading the same K/V.
     const uint32_t kvh = blockIdx.x % n_head_kv;
-    const size_t kv_dim = size_t(n_head_kv / kv_div) * kHeadDim;
+    const size_t kv_dim = size_t(n_head_kv / kv_div) * HD;
     uint32_t qblk = (n_tok + 16 * QW - 1) / (16 * QW), split = blockIdx.x / n_head_kv, n_splits = 1;
     uint32_t ntiles = 0;
     while (qblk > 0) {
@@ -126,26 +142,27 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     const uint32_t kend_w = q0 < n_tok ? pos + min(n_tok, q0 + 16) : 0;
     const uint32_t qpos = pos + q0 + li;  // this lane's query position
 
-    const _Float16* Kg = K + size_t(kvh / kv_div) * kHeadDim;
-    const _Float16* Vg = V + size_t(kvh / kv_div) * kHeadDim;
+    const _Float16* Kg = K + size_t(kvh / kv_div) * HD;
+    const _Float16* Vg = V + size_t(kvh / kv_div) * HD;
 
-    // Tile copy HBM -> LDS: 32 buffer_load ... lds instructions of 1 KB (4 rows) per tile,
-    // spread over the waves of the key group and issued in two groups between the compute
-    // phases of the current tile, so that the CU's address unit never receives all of them at
-    // once (a burst stalls every wave at the issue). Lane l of an instruction fills physical
-    // chunk l%16 of row 4*i + l/16, so it fetches the logical chunk (l%16) ^ swizzle(row). The
+    // Tile copy HBM -> LDS: 2*NIT buffer_load ... lds instructions of 1 KB (RPI rows) per tile
+    // (HD 128: 32 of 4 rows), spread over the waves of the key group and issued in two groups
+    // between the compute phases of the current tile, so that the CU's address unit never
+    // receives all of them at once (a burst stalls every wave at the issue). Lane l of
+    // instruction i fills physical chunk l%CPR of row RPI*(i%NIT) + l/CPR, so it fetches the
+    // logical chunk (l%CPR) ^ swizzle(row). The
     // per-lane byte offsets do not change from tile to tile; the buffer resource is rebased per
     // tile and its size covers only the visible rows, so rows past kend read as zeros (finite;
     // those keys are masked, so their P is exactly 0) with no clamping arithmetic.
-    constexpr int kInstPerWave = 32 / QW;  // each key group copies its own tiles
+    constexpr int kInstPerWave = 2 * NIT / QW;  // each key group copies its own tiles
     const uint32_t row_bytes = uint32_t(kv_dim) * 2;
     uint32_t dma_off[kInstPerWave];
 #pragma unroll
     for (int k = 0; k < kInstPerWave; k++) {
         const int i = qw + k * QW;
-        const int isv = i >> 4;
-        const int row = 4 * (i & 15) + (lane >> 4);
-        const int logical = (lane & 15) ^ (isv ? swz_v(row) : swz_k(row));
+        const int isv = i / NIT;
+        const int row = RPI * (i % NIT) + lane / CPR;
+        const int logical = (lane % CPR) ^ (isv ? swz_v<HD>(row) : swz_k<HD>(row));
         dma_off[k] = uint32_t(row) * row_bytes + 16u * uint32_t(logical);
     }
     // Copy instruction k (0 .. kInstPerWave-1) of this wave for tile t into buffer `buf`.
@@ -154,36 +171,37 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         char* stage = stage_of(kg, buf);
         const uint32_t nrec = min(kend - kb, uint32_t(kBN)) * row_bytes;
         const int i = qw + k * QW;  // wave-uniform
-        const int isv = i >> 4;
+        const int isv = i / NIT;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<_Float16*>((isv ? Vg : Kg) + size_t(kb) * kv_dim), 0, int(nrec), kBufferFlags);
-        char* dst = stage + isv * kTileBytes + (4 * (i & 15)) * kRowBytes;
+        char* dst = stage + isv * TB + (RPI * (i % NIT)) * RB;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)dst, 16, int(dma_off[k]), 0, 0, 0);
     };
 
     // Q is loaded once per workgroup: every thread converts part of the workgroup's
     // QW*16 queries x G heads (times scale*log2(e), to f16) into the second stage of each key
     // group, which the first tile's copy does not touch: queries 0..31 in key group 0's, 32..63
-    // in key group 1's, as rows [query][head][128 dims] with the 16-byte chunk c of a row stored
-    // at c ^ (query & 15), so that the B-operand reads below are bank-conflict free.
+    // in key group 1's, as rows [query][head][HD dims] with the 16-byte chunk c of a row stored
+    // at c ^ (query % CPR), so that the B-operand reads below are (nearly) bank-conflict free.
     // All of the thread's Q loads are issued first, then the first tile's copy: loads complete
     // in order, so the conversion waits only for Q, and the tile streams in meanwhile.
-    static_assert(QW * 16 == 64 && G * 32 * 256 <= kStageBytes, "Q staging fits the free stages");
-    constexpr int kF4 = QW * 16 * G * 32;  // float4 chunks of the workgroup's Q
+    static_assert(QW * 16 == 64 && G * 32 * RB <= SB, "Q staging fits the free stages");
+    constexpr int QF4 = HD / 4;            // float4 chunks of one (query, head) row
+    constexpr int kF4 = QW * 16 * G * QF4;  // float4 chunks of the workgroup's Q
     constexpr int NT = 64 * QW * KG;
     constexpr int kQIt = (kF4 + NT - 1) / NT;
     float4v qx[kQIt];
     {
         const __amdgpu_buffer_rsrc_t qr = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<float*>(q + size_t(qblk0) * q_stride + size_t(kvh) * G * kHeadDim), 0,
+            const_cast<float*>(q + size_t(qblk0) * q_stride + size_t(kvh) * G * HD), 0,
             0x7fffffff, kBufferFlags);
 #pragma unroll
         for (int it = 0; it < kQIt; it++) {
             const int idx = min(tid + it * NT, kF4 - 1);
-            const int ql = idx / (G * 32), rem = idx % (G * 32);
+            const int ql = idx / (G * QF4), rem = idx % (G * QF4);
             const uint32_t row = min(qblk0 + ql, n_tok - 1) - qblk0;
             qx[it] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
-                qr, int(4 * (row * q_stride + (rem >> 5) * kHeadDim + 4 * (rem & 31))), 0, 0));
+                qr, int(4 * (row * q_stride + (rem / QF4) * HD + 4 * (rem % QF4))), 0, 0));
         }
     }
     uint32_t t_first = t_begin + kg;
@@ -194,27 +212,27 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     for (int it = 0; it < kQIt; it++) {
         const int idx = tid + it * NT;
         if (kF4 % NT != 0 && idx >= kF4) break;
-        const int ql = idx / (G * 32), rem = idx % (G * 32);
-        const int h = rem >> 5, c4 = rem & 31;
+        const int ql = idx / (G * QF4), rem = idx % (G * QF4);
+        const int h = rem / QF4, c4 = rem % QF4;
         half4 y;
 #pragma unroll
         for (int e = 0; e < 4; e++) y[e] = _Float16(qx[it][e] * qscale);
         char* qs = stage_of(ql >> 5, 1);
-        const int chunk = (c4 >> 1) ^ (ql & 15);
-        *reinterpret_cast<half4*>(qs + ((ql & 31) * G + h) * kRowBytes + 16 * chunk + 8 * (c4 & 1)) = y;
+        const int chunk = (c4 >> 1) ^ (ql % CPR);
+        *reinterpret_cast<half4*>(qs + ((ql & 31) * G + h) * RB + 16 * chunk + 8 * (c4 & 1)) = y;
     }
     __syncthreads();
     // B operand Q^T per head: lane holds Q[q0 + li][32*ks + 8*g + e] * scale*log2(e), as f16.
-    half8 qb[G][4];
+    half8 qb[G][KS];
     {
         const int ql = 16 * qw + li;
-        const char* qs = stage_of(ql >> 5, 1) + (ql & 31) * G * kRowBytes;
+        const char* qs = stage_of(ql >> 5, 1) + (ql & 31) * G * RB;
 #pragma unroll
         for (int h = 0; h < G; h++)
 #pragma unroll
-            for (int ks = 0; ks < 4; ks++)
+            for (int ks = 0; ks < KS; ks++)
                 qb[h][ks] = *reinterpret_cast<const lds_half8*>(
-                    (const lds_void*)(qs + h * kRowBytes + 16 * ((4 * ks + g) ^ (ql & 15))));
+                    (const lds_void*)(qs + h * RB + 16 * ((4 * ks + g) ^ (ql % CPR))));
     }
 
     // Online-softmax state per head: reference max m (base 2), lane-partial row sum l, O^T.
@@ -222,7 +240,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // m only moves when some score exceeds it by more than kLazy (or for the first visible
     // keys), so P = 2^S' <= 2^kLazy and the O rescale is rare. O/l does not depend on the
     // reference, so this is exact.
-    float4v O[G][8];
+    float4v O[G][ND];
     float m[G], l[G];
     float4v negm[G];  // {-m, -m, -m, -m}: the C operand of the first score MFMA of each tile
     bool started[G];
@@ -234,7 +252,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         negm[h] = float4v{0.f, 0.f, 0.f, 0.f};
         started[h] = false;
 #pragma unroll
-        for (int d = 0; d < 8; d++) O[h][d] = float4v{0.f, 0.f, 0.f, 0.f};
+        for (int d = 0; d < ND; d++) O[h][d] = float4v{0.f, 0.f, 0.f, 0.f};
     }
 
     // `dma(k)` issues copy instruction k of the next tile (k < kInstPerWave).
@@ -247,7 +265,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             return;
         }
         const char* Ks = stage_of(kg, buf);
-        const char* Vs = Ks + kTileBytes;
+        const char* Vs = Ks + TB;
 
         // Two halves of 32 keys (scores, online-softmax update, P*V each), so only 32 keys'
         // worth of S and P is live at a time.
@@ -258,9 +276,9 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             for (int T = 0; T < 2; T++) {
                 const int row = 32 * hs + 16 * T + li;
 #pragma unroll
-                for (int ks = 0; ks < 4; ks++) {
-                    const int chunk = (4 * ks + g) ^ swz_k(row);
-                    const half8 a = *reinterpret_cast<const lds_half8*>((const lds_void*)(Ks + row * kRowBytes + 16 * chunk));
+                for (int ks = 0; ks < KS; ks++) {
+                    const int chunk = (4 * ks + g) ^ swz_k<HD>(row);
+                    const half8 a = *reinterpret_cast<const lds_half8*>((const lds_void*)(Ks + row * RB + 16 * chunk));
 #pragma unroll
                     for (int h = 0; h < G; h++)
                         S[T][h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[h][ks], ks == 0 ? negm[h] : S[T][h], 0, 0, 0);
@@ -314,7 +332,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
 #pragma unroll
                     for (int T = 0; T < 2; T++) S[T][h] -= delta;
 #pragma unroll
-                    for (int d = 0; d < 8; d++) O[h][d] *= alpha;
+                    for (int d = 0; d < ND; d++) O[h][d] *= alpha;
                 }
                 all_started = __builtin_amdgcn_ballot_w64(pending) == 0;
             }
@@ -337,7 +355,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         auto pv = [&](int hs, const half8 (&Pp)[G]) {
             // O^T (128 dims x (G x 16 queries)) += V^T (128 x 32) P^T (32 x 16) per head.
 #pragma unroll
-            for (int d = 0; d < 8; d++) {
+            for (int d = 0; d < ND; d++) {
                 half4 part_[2];
 #pragma unroll
                 for (int half_ = 0; half_ < 2; half_++) {
@@ -345,8 +363,8 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                     const int key0 = 32 * hs + 16 * half_ + 4 * g;
                     const int row = key0 + (li >> 2);
                     const int byte = 32 * d + 8 * (li & 3);
-                    const int chunk = (byte >> 4) ^ swz_v(row);
-                    lds_fp16x4* src = (lds_fp16x4*)(lds_void*)const_cast<char*>(Vs + row * kRowBytes + 16 * chunk + (byte & 15));
+                    const int chunk = (byte >> 4) ^ swz_v<HD>(row);
+                    lds_fp16x4* src = (lds_fp16x4*)(lds_void*)const_cast<char*>(Vs + row * RB + 16 * chunk + (byte & 15));
                     part_[half_] = __builtin_bit_cast(half4, __builtin_amdgcn_ds_read_tr16_b64_v4f16(src));
                 }
                 const half8 a = __builtin_shufflevector(part_[0], part_[1], 0, 1, 2, 3, 4, 5, 6, 7);
@@ -367,7 +385,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         // scores) to land before its P*V, and the next tile's start is not held up. (Copies
         // issued among the P*V reads made C5 1.9x slower; all 8 after the first half measured
         // like this split within 1%.)
-        static_assert(kInstPerWave == 8, "two groups of 4 copies");
+        static_assert(kInstPerWave % 2 == 0, "two groups of copies");
         __builtin_amdgcn_s_setprio(1);
         scores(0);
         __builtin_amdgcn_s_setprio(0);
@@ -376,20 +394,20 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         pv(0, P);
         __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-        for (int k = 0; k < 4; k++) dma(k);
+        for (int k = 0; k < kInstPerWave / 2; k++) dma(k);
         if (kb + 32 < kend_w) {
             __builtin_amdgcn_s_setprio(1);
             scores(1);
             __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-            for (int k = 4; k < 8; k++) dma(k);
+            for (int k = kInstPerWave / 2; k < kInstPerWave; k++) dma(k);
             softmax(1);
             __builtin_amdgcn_s_setprio(1);
             pv(1, P);
             __builtin_amdgcn_s_setprio(0);
         } else {
 #pragma unroll
-            for (int k = 4; k < 8; k++) dma(k);
+            for (int k = kInstPerWave / 2; k < kInstPerWave; k++) dma(k);
         }
     };
 
@@ -427,14 +445,14 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         // its (O, m, l, started) per lane for every head, one barrier, group 0 folds them in
         // with the log-sum-exp rule. Head h's O goes to stage object h (8 16-byte fields x 64
         // lanes x QW waves = one stage), its (m, l) to mlx; lane-minor, conflict-free.
-        static_assert(G <= 4 && QW * 8 * 64 * 16 == kStageBytes, "merge buffers");
+        static_assert(G <= 4 && QW * ND * 64 * 16 == SB, "merge buffers");
         {
             if (kg == 1) {
 #pragma unroll
                 for (int h = 0; h < G; h++) {
-                    float4v* st = reinterpret_cast<float4v*>(stage_of(h >> 1, h & 1)) + qw * 8 * 64 + lane;
+                    float4v* st = reinterpret_cast<float4v*>(stage_of(h >> 1, h & 1)) + qw * ND * 64 + lane;
 #pragma unroll
-                    for (int d = 0; d < 8; d++) st[d * 64] = O[h][d];
+                    for (int d = 0; d < ND; d++) st[d * 64] = O[h][d];
                     mlx[h][qw][lane] = float4v{m[h], l[h], started[h] ? 1.f : 0.f, 0.f};
                 }
             }
@@ -442,7 +460,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             if (kg == 0) {
 #pragma unroll
                 for (int h = 0; h < G; h++) {
-                    const float4v* st = reinterpret_cast<const float4v*>(stage_of(h >> 1, h & 1)) + qw * 8 * 64 + lane;
+                    const float4v* st = reinterpret_cast<const float4v*>(stage_of(h >> 1, h & 1)) + qw * ND * 64 + lane;
                     const float4v ml = mlx[h][qw][lane];
                     const float m1 = ml[0], l1 = ml[1];
                     const bool s1 = ml[2] != 0.f;
@@ -450,7 +468,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                     const float a0 = started[h] ? fast_exp2(m[h] - M) : 0.f;
                     const float a1 = s1 ? fast_exp2(m1 - M) : 0.f;
 #pragma unroll
-                    for (int d = 0; d < 8; d++) O[h][d] = O[h][d] * a0 + st[d * 64] * a1;
+                    for (int d = 0; d < ND; d++) O[h][d] = O[h][d] * a0 + st[d * 64] * a1;
                     l[h] = l[h] * a0 + l1 * a1;
                     m[h] = (started[h] || s1) ? M : m[h];
                     started[h] = started[h] || s1;
@@ -473,31 +491,34 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         const uint32_t head = kvh * G + h;
         if (n_splits == 1) {
             const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
-            float* dst = out + size_t(row) * q_stride + size_t(head) * kHeadDim + 4 * g;
+            float* dst = out + size_t(row) * q_stride + size_t(head) * HD + 4 * g;
 #pragma unroll
-            for (int d = 0; d < 8; d++) *reinterpret_cast<float4v*>(dst + 16 * d) = O[h][d] * inv;
+            for (int d = 0; d < ND; d++) *reinterpret_cast<float4v*>(dst + 16 * d) = O[h][d] * inv;
         } else {
             const uint32_t n_head = n_head_kv * G;
             float* dst = part + ((size_t(split) * n_tok + row) * n_head + head) * kPartStride;
 #pragma unroll
-            for (int d = 0; d < 8; d++) *reinterpret_cast<float4v*>(dst + 16 * d + 4 * g) = O[h][d];
+            for (int d = 0; d < ND; d++) *reinterpret_cast<float4v*>(dst + 16 * d + 4 * g) = O[h][d];
             // a query that saw no key in this split contributes nothing: report m = -inf-like
-            if (g == 0) *reinterpret_cast<float4v*>(dst + 128) = float4v{started[h] ? m[h] : kNoMax, l[h], 0.f, 0.f};
+            if (g == 0) *reinterpret_cast<float4v*>(dst + HD) = float4v{started[h] ? m[h] : kNoMax, l[h], 0.f, 0.f};
         }
     }
 }
 
 // out[tok][h][d] = sum_s o_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M); 0 if the sum is 0 — the
 // log-sum-exp merge of attn_combine (shaders/kernels.metal:501-516) over the split records.
-// 32 threads per (token, head) record, each owning 4 dims; the loads of 4 splits are in flight
-// at once and folded in online (clamped indices keep them unconditional, masked entries get
-// weight 0).
+// HD/4 threads per (token, head) record, each owning 4 dims; the loads of 4 splits are in
+// flight at once and folded in online (clamped indices keep them unconditional, masked entries
+// get weight 0). A record is kPartStride floats: o[HD], then m and l.
 constexpr int kCombineThreads = 256;
 constexpr uint32_t kQBlock = 64;  // queries per prefill workgroup (16 x kQW)
+template <int HD>
 __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
     const float* __restrict__ part, float* __restrict__ out, uint32_t pos, uint32_t n_tok,
     uint32_t n_head, uint32_t q_stride, uint32_t tps) {
-    const uint32_t rec = blockIdx.x * (kCombineThreads / 32) + threadIdx.x / 32;
+    constexpr int TPR = HD / 4;  // threads per record
+    static_assert(HD + 2 <= kPartStride, "record fits");
+    const uint32_t rec = blockIdx.x * (kCombineThreads / TPR) + threadIdx.x / TPR;
     if (rec >= n_tok * n_head) return;
     const uint32_t row = rec / n_head, h = rec % n_head;
     // The split count of this token's query block, as the prefill kernel enumerates it; blocks
@@ -505,7 +526,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
     const uint32_t blk_end = min(n_tok, (row / kQBlock + 1) * kQBlock);
     const uint32_t n_splits = ((pos + blk_end + kBN - 1) / kBN + tps - 1) / tps;
     if (n_splits == 1) return;
-    const int d = 4 * (threadIdx.x % 32);
+    const int d = 4 * (threadIdx.x % TPR);
     const size_t sstride = size_t(n_tok) * n_head * kPartStride;
     const float* src = part + size_t(rec) * kPartStride;
     float M = kNoMax, L = 0.f;
@@ -516,8 +537,8 @@ __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float* ps = src + min(s0 + u, n_splits - 1) * sstride;
-            ms[u] = s0 + u < n_splits ? ps[128] : kNoMax;
-            ls[u] = ps[129];
+            ms[u] = s0 + u < n_splits ? ps[HD] : kNoMax;
+            ls[u] = ps[HD + 1];
             os[u] = *reinterpret_cast<const float4v*>(ps + d);
         }
 #pragma unroll
@@ -530,13 +551,13 @@ __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
         }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    *reinterpret_cast<float4v*>(out + size_t(row) * q_stride + size_t(h) * kHeadDim + d) = O * inv;
+    *reinterpret_cast<float4v*>(out + size_t(row) * q_stride + size_t(h) * HD + d) = O * inv;
 }
 
 constexpr int kQW = 4;  // query waves per workgroup (16 queries x G heads each)
 constexpr int kKG = 2;  // key groups per workgroup (alternate tiles, merged through LDS)
 
-template <int G>
+template <int HD, int G>
 int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                      uint32_t kv_div, uint32_t n_splits, float qscale, hipStream_t stream) {
@@ -550,13 +571,13 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
     }
     if (uint64_t(pairs) * n_head_kv > 0x7fffffffu) return -1;
     const dim3 grid(pairs * n_head_kv);
-    hipLaunchKernelGGL((attn_prefill_kernel<G, kQW, kKG>), grid, dim3(64 * kQW * kKG), 0, stream,
+    hipLaunchKernelGGL((attn_prefill_kernel<HD, G, kQW, kKG>), grid, dim3(64 * kQW * kKG), 0, stream,
                        q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, kv_div, tps, qscale);
     if (hipGetLastError() != hipSuccess) return -4;
     if (n_splits > 1) {
         const uint32_t n_head = n_head_kv * G;
-        const uint32_t per_block = kCombineThreads / 32;
-        hipLaunchKernelGGL(attn_prefill_combine, dim3((n_tok * n_head + per_block - 1) / per_block),
+        const uint32_t per_block = kCombineThreads / (HD / 4);
+        hipLaunchKernelGGL(attn_prefill_combine<HD>, dim3((n_tok * n_head + per_block - 1) / per_block),
                            dim3(kCombineThreads), 0, stream, part,
                            out, pos, n_tok, n_head, q_stride, tps);
         if (hipGetLastError() != hipSuccess) return -4;
@@ -607,9 +628,12 @@ uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32
     return (max_tiles + tps - 1) / tps;
 }
 
-int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
-                   uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
-                   uint32_t group, uint32_t n_splits, float scale, hipStream_t stream) {
+namespace {
+
+template <int HD>
+int launch_prefill_hd(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
+                      uint32_t group, uint32_t n_splits, float scale, hipStream_t stream) {
     const float qscale = scale * kLog2e;
     // A chunk that gives fewer workgroups than the chip has CUs and needs no key split runs
     // every query head of a group in its own workgroup (G = 1 over n_head_kv * group units):
@@ -618,15 +642,28 @@ int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* 
     // is shorter (the K/V tile is then read from L2 once per head instead of once per group).
     const uint32_t blocks = (n_tok + kQBlock - 1) / kQBlock;
     if (group > 1 && n_splits == 1 && uint64_t(blocks) * n_head_kv * group <= 256)
-        return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv * group, group,
-                                   1, qscale, stream);
+        return launch_prefill_g<HD, 1>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv * group,
+                                       group, 1, qscale, stream);
     // Groups above 3 run as units of gs heads (the largest divisor of the group up to 3), kv_div of
     // them per KV head, each reading that head's K/V.
     const uint32_t gs = prefill_unit_heads(group), kv_div = group / gs, units = n_head_kv * kv_div;
     switch (gs) {
-        case 1: return launch_prefill_g<1>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
-        case 2: return launch_prefill_g<2>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
-        case 3: return launch_prefill_g<3>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        case 1: return launch_prefill_g<HD, 1>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        case 2: return launch_prefill_g<HD, 2>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        case 3: return launch_prefill_g<HD, 3>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        default: return -2;
+    }
+}
+
+}  // namespace
+
+int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+                   uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
+                   uint32_t group, uint32_t head_dim, uint32_t n_splits, float scale,
+                   hipStream_t stream) {
+    switch (head_dim) {
+        case 64: return launch_prefill_hd<64>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, group, n_splits, scale, stream);
+        case 128: return launch_prefill_hd<128>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, group, n_splits, scale, stream);
         default: return -2;
     }
 }
