@@ -30,8 +30,8 @@
  * and prefill (the reference's flash kernels cover head_dim 128 — decode with groups up to 4,
  * src/metal_backend.mm:339, prefill any group, :360 — and its naive kernel every other shape,
  * src/metal_backend.mm:373-382). head_dim 128 runs the tuned decode kernel (groups 1..4,
- * attn_decode.hip); head_dim 64 and 128 prefill run the MFMA kernel in units of up to 3 heads;
- * the other shapes run the generic kernel. At most 256 query heads (one workspace counter each). Llama-3.2-3B is 24 Q heads /
+ * attn_decode.hip), other decode shapes the generic decode kernel; prefill of every head size
+ * runs the MFMA kernel (units of up to 3 heads, 1 at head_dim 256). At most 256 query heads (one workspace counter each). Llama-3.2-3B is 24 Q heads /
  * 8 KV heads (group 3); Llama-3.2-1B 32 / 8 with head_dim 64.
  */
 #ifndef INGOT_ATTN_H

@@ -16,7 +16,6 @@
 namespace {
 
 using ingot::kCounterBytes;
-constexpr size_t kPartFloats = 132;     // per-(split, head) partial record, as in the kernels
 
 size_t prefill_part_offset(uint32_t n_head) { return kCounterBytes + size_t(n_head) * ingot::kDecodeHeadRecordBytes; }
 
@@ -198,13 +197,11 @@ uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
     return ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
 }
 
-// Prefill split count: the MFMA kernel's (head_dim 64 and 128) over its workgroup units; the
-// other head size runs unsplit.
+// Prefill split count of the MFMA kernel over its workgroup units.
 uint32_t prefill_split_count(const IngotAttnPrefillDesc* d) {
-    if (!ingot::prefill_mfma_head_dim(d->head_dim)) return 1;
     const uint32_t group = d->n_head / d->n_head_kv;
-    const uint32_t units = d->n_head_kv * (group / ingot::prefill_unit_heads(group));
-    return ingot::prefill_splits(d->pos, d->n_tok, units, d->n_splits);
+    const uint32_t units = d->n_head_kv * (group / ingot::prefill_unit_heads(group, d->head_dim));
+    return ingot::prefill_splits(d->pos, d->n_tok, units, d->head_dim, d->n_splits);
 }
 
 uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
@@ -221,7 +218,8 @@ size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
 size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d) {
     if (check_prefill(d)) return 0;
     const uint32_t splits = prefill_split_count(d);
-    const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head * kPartFloats * sizeof(float) : 0;
+    const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head *
+                                          ingot::prefill_record_floats(d->head_dim) * sizeof(float) : 0;
     // The prefill records follow the decode record regions of the same heads, so a workspace
     // shared by decode and prefill calls never holds prefill data where decode tags are read.
     return prefill_part_offset(d->n_head) + parts;
@@ -260,16 +258,10 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
     const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
     const hipStream_t st = static_cast<hipStream_t>(stream);
-    int lrc;
-    if (ingot::prefill_mfma_head_dim(d->head_dim)) {
-        const uint32_t splits = prefill_split_count(d);
-        auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_part_offset(d->n_head));
-        lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
-                                    d->n_head / d->n_head_kv, d->head_dim, splits, d->scale, st);
-    } else {
-        lrc = ingot::launch_prefill_any(q, k, v, out, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
-                                        d->n_head / d->n_head_kv, d->head_dim, d->scale, st);
-    }
+    const uint32_t splits = prefill_split_count(d);
+    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_part_offset(d->n_head));
+    const int lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
+                                          d->n_head / d->n_head_kv, d->head_dim, splits, d->scale, st);
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
          : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }

@@ -217,7 +217,7 @@ __device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uin
 template <int HD, int G>
 __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
-    float* __restrict__ out, char* __restrict__ recs, uint32_t pos0, uint32_t n_tok, uint32_t q_stride,
+    float* __restrict__ out, char* __restrict__ recs, uint32_t n_keys,
     uint32_t keys_per_split, uint32_t n_splits, uint32_t n_units, uint32_t n_sub, uint32_t kv_dim,
     uint32_t group, float qscale) {
     static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim 64, 128 or 256");
@@ -232,9 +232,8 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t per_tok = n_splits * n_units;  // walkers per query token
-    const uint32_t n_walk = per_tok * n_tok;
-    if (blockIdx.x >= n_walk) {  // (several slices only with one token: decode)
+    const uint32_t n_walk = n_splits * n_units;
+    if (blockIdx.x >= n_walk) {
         const uint32_t m = blockIdx.x - n_walk, unit = m % n_units, h = m / n_units;
         const bool near = (n_units & 7) == 0 && xcc_id() == (blockIdx.x & 7);
         merge_head<HD>(recs, out, (unit / n_sub) * group + (unit % n_sub) * G + h, n_splits, near, lane, wave);
@@ -247,13 +246,7 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
 
     const int ki = lane & 15, kg = lane >> 4;         // MFMA lane coordinates
     const int vc = lane % CPR, vr = lane / CPR;       // V chunk and key sub-row of the lane
-    // Query token `token` sits at position pos0 + token and sees keys 0 .. pos0 + token (a decode
-    // call is the one token at pos0 = n_keys - 1; a prefill chunk runs unsplit, token by token).
-    const uint32_t token = blockIdx.x / per_tok, in_tok = blockIdx.x % per_tok;
-    const uint32_t n_keys = pos0 + token + 1;
-    q += size_t(token) * q_stride;
-    out += size_t(token) * q_stride;
-    const uint32_t unit = in_tok % n_units, split = in_tok / n_units;
+    const uint32_t unit = blockIdx.x % n_units, split = blockIdx.x / n_units;
     const uint32_t kvh = unit / n_sub, sub = unit % n_sub;
     const uint32_t head0 = kvh * group + sub * G;     // first query head of the unit
     const uint32_t k0 = split * keys_per_split;
@@ -448,22 +441,22 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
 
 template <int HD, int G>
 void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
-              const _Float16* v, float* out, char* recs, uint32_t pos0, uint32_t n_tok,
-              uint32_t q_stride, uint32_t per, uint32_t n_splits, uint32_t n_units, uint32_t n_sub,
+              const _Float16* v, float* out, char* recs, uint32_t n_keys,
+              uint32_t per, uint32_t n_splits, uint32_t n_units, uint32_t n_sub,
               uint32_t kv_dim, uint32_t group, float qscale) {
     hipLaunchKernelGGL((attn_decode_kernel<HD, G>), dim3(n_blocks), dim3(64 * kNW), 0, stream, q, k, v,
-                       out, recs, pos0, n_tok, q_stride, per, n_splits, n_units, n_sub, kv_dim, group,
+                       out, recs, n_keys, per, n_splits, n_units, n_sub, kv_dim, group,
                        qscale);
 }
 
 template <int HD>
 int launch_hd(uint32_t gs, uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
-              const _Float16* v, float* out, char* recs, uint32_t pos0, uint32_t n_tok,
-              uint32_t q_stride, uint32_t per, uint32_t n_splits, uint32_t n_units, uint32_t n_sub,
+              const _Float16* v, float* out, char* recs, uint32_t n_keys,
+              uint32_t per, uint32_t n_splits, uint32_t n_units, uint32_t n_sub,
               uint32_t kv_dim, uint32_t group, float qscale) {
 #define INGOT_DECODE_G(GG)                                                                         \
     case GG:                                                                                       \
-        launch_g<HD, GG>(n_blocks, stream, q, k, v, out, recs, pos0, n_tok, q_stride, per,        \
+        launch_g<HD, GG>(n_blocks, stream, q, k, v, out, recs, n_keys, per,                       \
                          n_splits, n_units, n_sub, kv_dim, group, qscale);                        \
         return 0;
     switch (gs) {
@@ -512,15 +505,15 @@ uint32_t decode_splits(uint32_t n_keys, uint32_t head_dim, uint32_t requested) {
 
 namespace {
 
-// Any shape, `n_tok` query tokens at positions pos0..pos0+n_tok-1 (decode: one token, n_splits
-// slices; prefill: n_splits = 1).
-int launch_any(const float* q, const _Float16* k, const _Float16* v, float* out, void* recs, uint32_t pos0,
-               uint32_t n_tok, uint32_t q_stride, uint32_t per, uint32_t n_splits, uint32_t n_head_kv,
-               uint32_t group, uint32_t head_dim, float scale, hipStream_t stream) {
+}  // namespace
+
+int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, float* out, void* recs,
+                      uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
+                      uint32_t head_dim, float scale, hipStream_t stream) {
+    const uint32_t per = (n_keys + n_splits - 1) / n_splits;
     const uint32_t gs = decode_unit_heads(group);
     const uint32_t n_sub = group / gs, n_units = n_head_kv * n_sub;
-    const uint64_t blocks =
-        uint64_t(n_splits) * n_units * n_tok + (n_splits > 1 ? uint64_t(n_units) * gs : 0);
+    const uint64_t blocks = uint64_t(n_splits) * n_units + (n_splits > 1 ? uint64_t(n_units) * gs : 0);
     if (blocks > 0x7fffffffu) return -1;
     const uint32_t kv_dim = n_head_kv * head_dim;
     const float qscale = scale * kLog2e;
@@ -528,30 +521,13 @@ int launch_any(const float* q, const _Float16* k, const _Float16* v, float* out,
     const uint32_t nb = uint32_t(blocks);
     int rc;
     switch (head_dim) {
-        case 64: rc = launch_hd<64>(gs, nb, stream, q, k, v, out, r, pos0, n_tok, q_stride, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
-        case 128: rc = launch_hd<128>(gs, nb, stream, q, k, v, out, r, pos0, n_tok, q_stride, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
-        case 256: rc = launch_hd<256>(gs, nb, stream, q, k, v, out, r, pos0, n_tok, q_stride, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
+        case 64: rc = launch_hd<64>(gs, nb, stream, q, k, v, out, r, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
+        case 128: rc = launch_hd<128>(gs, nb, stream, q, k, v, out, r, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
+        case 256: rc = launch_hd<256>(gs, nb, stream, q, k, v, out, r, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
         default: return -2;
     }
     if (rc) return rc;
     return hipGetLastError() == hipSuccess ? 0 : -4;
-}
-
-}  // namespace
-
-int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, float* out, void* recs,
-                      uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
-                      uint32_t head_dim, float scale, hipStream_t stream) {
-    const uint32_t per = (n_keys + n_splits - 1) / n_splits;
-    return launch_any(q, k, v, out, recs, n_keys - 1, 1, n_head_kv * group * head_dim, per, n_splits, n_head_kv,
-                      group, head_dim, scale, stream);
-}
-
-int launch_prefill_any(const float* q, const _Float16* k, const _Float16* v, float* out, uint32_t pos,
-                       uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv, uint32_t group,
-                       uint32_t head_dim, float scale, hipStream_t stream) {
-    return launch_any(q, k, v, out, nullptr, pos, n_tok, q_stride, 0xffffffffu, 1, n_head_kv, group, head_dim,
-                      scale, stream);
 }
 
 int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* out, void* workspace,

@@ -30,10 +30,13 @@ constexpr size_t kDecodeHeadRecordBytes = 32 * 528;
 static_assert(kDecodeHeadRecordBytes >= 32 * decode_record_bytes(64) &&
               kDecodeHeadRecordBytes >= 32 * decode_record_bytes(128) &&
               kDecodeHeadRecordBytes >= 16 * decode_record_bytes(256), "decode record region");
-// Prefill: split count (n_units = workgroup units: KV heads x group / prefill_unit_heads(group))
-// and the query heads one MFMA-prefill unit serves (a divisor of the group, at most 4).
-uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_units, uint32_t requested);
-uint32_t prefill_unit_heads(uint32_t group);
+// Prefill: split count (n_units = workgroup units: KV heads x group / prefill_unit_heads) and
+// the query heads one MFMA-prefill unit serves (a divisor of the group: at most 3, 1 for
+// head_dim 256). A split record is head_dim + 4 floats.
+uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_units, uint32_t head_dim,
+                        uint32_t requested);
+uint32_t prefill_unit_heads(uint32_t group, uint32_t head_dim);
+constexpr size_t prefill_record_floats(uint32_t head_dim) { return head_dim + 4; }
 
 // Decode attention, dispatched by launch_decode: head_dim 128 with groups 1..4 take the tuned
 // kernel (attn_decode.hip; completion counters in the workspace's first kCounterBytes, records
@@ -48,18 +51,11 @@ int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, flo
 int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, float* out, void* recs,
                       uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
                       uint32_t head_dim, float scale, hipStream_t stream);
-// Prefill for the shapes the MFMA prefill kernel does not take (head_dim 256): every token of
-// the chunk through the generic kernel, unsplit (attn_decode_any.hip).
-int launch_prefill_any(const float* q, const _Float16* k, const _Float16* v, float* out, uint32_t pos,
-                       uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv, uint32_t group,
-                       uint32_t head_dim, float scale, hipStream_t stream);
-// The MFMA prefill kernel (attn_prefill.hip), head_dim 64 or 128.
+// The MFMA prefill kernel (attn_prefill.hip), head_dim 64, 128 or 256.
 int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
                    uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                    uint32_t group, uint32_t head_dim, uint32_t n_splits, float scale,
                    hipStream_t stream);
-// head_dim taken by launch_prefill
-inline bool prefill_mfma_head_dim(uint32_t head_dim) { return head_dim == 64 || head_dim == 128; }
 
 // RoPE on q (in place, skipped when q is null) and k; K and V as f16 into the cache rows.
 // Returns 0, -1 (grid too large) or -4 (launch failed).

@@ -47,14 +47,15 @@ typedef __fp16 fp16x4 __attribute__((__vector_size__(8)));  // operand type of d
 typedef __attribute__((address_space(3))) fp16x4 lds_fp16x4;
 typedef __attribute__((address_space(3))) half8 lds_half8;
 
-constexpr int kBN = 64;                        // keys per tile
+// Keys per tile: 64, or 32 for head_dim 256 (four 64 KB stages would not fit the LDS).
+template <int HD> constexpr int kBN = HD == 256 ? 32 : 64;
 constexpr float kLazy = 8.f;                   // base-2 headroom before the reference max moves
 constexpr int kBufferFlags = 0x00020000;       // buffer descriptor word 3 (raw, 32-bit format)
 // LDS geometry for head size HD: a K/V row of HD halves (no padding), 16-byte chunks per row,
 // a K or V tile of kBN rows, a stage = K tile + V tile (HD 128: 256 B, 16, 16 KB, 32 KB).
 template <int HD> constexpr int kRowBytes = HD * 2;
 template <int HD> constexpr int kChunks = HD / 8;
-template <int HD> constexpr int kTileBytes = kBN * kRowBytes<HD>;
+template <int HD> constexpr int kTileBytes = kBN<HD> * kRowBytes<HD>;
 template <int HD> constexpr int kStageBytes = 2 * kTileBytes<HD>;
 
 // Max over the 4 lanes l, l^16, l^32, l^48 (the lanes that hold one query column) with the
@@ -72,8 +73,8 @@ __device__ __forceinline__ float max_lanes4(float x) {
 // XOR swizzles of the 16-byte chunk index inside a row, chosen so that the 16 lanes of a
 // 16-byte K read (16 rows, one logical chunk) and the 32 lanes of a transposing V read (8 rows,
 // a 32-byte chunk pair each) cover all 64 banks once. A 256-byte row spans the 64 banks, so
-// the chunk (pair) index alone must differ; a 128-byte row spans half of them, so rows of the
-// same parity must differ, hence row >> 1.
+// the chunk (pair) index alone must differ (a 512-byte row: its low bits); a 128-byte row spans
+// half of them, so rows of the same parity must differ, hence row >> 1.
 template <int HD> __device__ __forceinline__ int swz_k(int row) {
     return HD == 64 ? (row >> 1) & 7 : row & 15;
 }
@@ -87,7 +88,9 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                          const _Float16* __restrict__ V, float* __restrict__ out,
                          float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
                          uint32_t n_head_kv, uint32_t kv_div, uint32_t tps, float qscale) {
-    constexpr int RB = kRowBytes<HD>, CPR = kChunks<HD>, TB = kTileBytes<HD>, SB = kStageBytes<HD>;
+    constexpr int BN = kBN<HD>, RB = kRowBytes<HD>, CPR = kChunks<HD>, TB = kTileBytes<HD>, SB = kStageBytes<HD>;
+    constexpr int HALVES = BN / 32;  // 32-key halves per tile
+    constexpr int PS = HD + 4;       // floats per split record: o[HD], m, l (16-byte aligned)
     constexpr int NIT = TB / 1024;  // 1 KB copy instructions per K (or V) tile
     constexpr int RPI = 1024 / RB;  // rows per copy instruction
     constexpr int KS = HD / 32;     // 32-wide k steps of a score MFMA chain
@@ -124,7 +127,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     uint32_t ntiles = 0;
     while (qblk > 0) {
         qblk--;
-        ntiles = (pos + min(n_tok, (qblk + 1) * 16 * QW) + kBN - 1) / kBN;
+        ntiles = (pos + min(n_tok, (qblk + 1) * 16 * QW) + BN - 1) / BN;
         n_splits = (ntiles + tps - 1) / tps;
         if (split < n_splits) break;
         split -= n_splits;
@@ -167,9 +170,9 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     }
     // Copy instruction k (0 .. kInstPerWave-1) of this wave for tile t into buffer `buf`.
     auto issue_inst = [&](uint32_t t, int buf, int k) {
-        const uint32_t kb = t * kBN;
+        const uint32_t kb = t * BN;
         char* stage = stage_of(kg, buf);
-        const uint32_t nrec = min(kend - kb, uint32_t(kBN)) * row_bytes;
+        const uint32_t nrec = min(kend - kb, uint32_t(BN)) * row_bytes;
         const int i = qw + k * QW;  // wave-uniform
         const int isv = i / NIT;
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -258,7 +261,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     // `dma(k)` issues copy instruction k of the next tile (k < kInstPerWave).
     auto compute_tile = [&](uint32_t t, auto bufc, auto&& dma) {
         constexpr int buf = decltype(bufc)::value;
-        const uint32_t kb = t * kBN;
+        const uint32_t kb = t * BN;
         if (kb >= kend_w) {  // every key of this tile is in this wave's future
 #pragma unroll
             for (int k = 0; k < kInstPerWave; k++) dma(k);
@@ -267,8 +270,8 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         const char* Ks = stage_of(kg, buf);
         const char* Vs = Ks + TB;
 
-        // Two halves of 32 keys (scores, online-softmax update, P*V each), so only 32 keys'
-        // worth of S and P is live at a time.
+        // Halves of 32 keys (scores, online-softmax update, P*V each), so only 32 keys' worth
+        // of S and P is live at a time.
         float4v S[2][G];
         half8 P[G];
         auto scores = [&](int hs) {
@@ -378,36 +381,51 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
         // switches break the lockstep of the two waves on a SIMD (which the per-tile barrier
         // restores), so one wave's VALU work lines up more often with the other's matrix work
         // (measured: C5 187.8 -> 182.6 us; which phase gets the priority makes no difference).
-        // The next tile's copy goes out in two halves of 4 instructions: after the first P*V
+        // The next tile's copy goes out in two groups of instructions: after the first P*V
         // half and after the second half's scores. The compiler waits for every copy in flight
         // before a transposing LDS read (it cannot tell them apart), so no copy may be issued
         // before or among the first half's reads; these have the second half's softmax (and
         // scores) to land before its P*V, and the next tile's start is not held up. (Copies
-        // issued among the P*V reads made C5 1.9x slower; all 8 after the first half measured
-        // like this split within 1%.)
+        // issued among the P*V reads made C5 1.9x slower; all of them after the first half
+        // measured like this split within 1%.) A one-half tile (head_dim 256) issues them
+        // before its scores and softmax, and its P*V waits for them.
         static_assert(kInstPerWave % 2 == 0, "two groups of copies");
-        __builtin_amdgcn_s_setprio(1);
-        scores(0);
-        __builtin_amdgcn_s_setprio(0);
-        softmax(0);
-        __builtin_amdgcn_s_setprio(1);
-        pv(0, P);
-        __builtin_amdgcn_s_setprio(0);
+        if constexpr (HALVES == 1) {
 #pragma unroll
-        for (int k = 0; k < kInstPerWave / 2; k++) dma(k);
-        if (kb + 32 < kend_w) {
+            for (int k = 0; k < kInstPerWave / 2; k++) dma(k);
             __builtin_amdgcn_s_setprio(1);
-            scores(1);
+            scores(0);
             __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int k = kInstPerWave / 2; k < kInstPerWave; k++) dma(k);
-            softmax(1);
+            softmax(0);
             __builtin_amdgcn_s_setprio(1);
-            pv(1, P);
+            pv(0, P);
             __builtin_amdgcn_s_setprio(0);
         } else {
+            __builtin_amdgcn_s_setprio(1);
+            scores(0);
+            __builtin_amdgcn_s_setprio(0);
+            softmax(0);
+            __builtin_amdgcn_s_setprio(1);
+            pv(0, P);
+            __builtin_amdgcn_s_setprio(0);
 #pragma unroll
-            for (int k = kInstPerWave / 2; k < kInstPerWave; k++) dma(k);
+            for (int k = 0; k < kInstPerWave / 2; k++) dma(k);
+            if (kb + 32 < kend_w) {
+                __builtin_amdgcn_s_setprio(1);
+                scores(1);
+                __builtin_amdgcn_s_setprio(0);
+#pragma unroll
+                for (int k = kInstPerWave / 2; k < kInstPerWave; k++) dma(k);
+                softmax(1);
+                __builtin_amdgcn_s_setprio(1);
+                pv(1, P);
+                __builtin_amdgcn_s_setprio(0);
+            } else {
+#pragma unroll
+                for (int k = kInstPerWave / 2; k < kInstPerWave; k++) dma(k);
+            }
         }
     };
 
@@ -443,16 +461,22 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     if (KG == 2) {
         // Merge the two key groups through LDS (the tiles are no longer read): group 1 stores
         // its (O, m, l, started) per lane for every head, one barrier, group 0 folds them in
-        // with the log-sum-exp rule. Head h's O goes to stage object h (8 16-byte fields x 64
-        // lanes x QW waves = one stage), its (m, l) to mlx; lane-minor, conflict-free.
-        static_assert(G <= 4 && QW * ND * 64 * 16 == SB, "merge buffers");
+        // with the log-sum-exp rule. O field f = h*ND + d (16 bytes per lane, QW waves x 64
+        // lanes, lane-minor: conflict-free) goes to stage object f / FPS, slot f % FPS; (m, l)
+        // to mlx.
+        constexpr int FPS = SB / (QW * 64 * 16);  // O fields per stage object
+        static_assert(G * ND <= 4 * FPS, "merge buffers");
+        auto field = [&](int h, int d) -> float4v* {
+            const int f = h * ND + d;
+            return reinterpret_cast<float4v*>(stage_of((f / FPS) >> 1, (f / FPS) & 1)) +
+                   ((f % FPS) * QW + qw) * 64 + lane;
+        };
         {
             if (kg == 1) {
 #pragma unroll
                 for (int h = 0; h < G; h++) {
-                    float4v* st = reinterpret_cast<float4v*>(stage_of(h >> 1, h & 1)) + qw * ND * 64 + lane;
 #pragma unroll
-                    for (int d = 0; d < ND; d++) st[d * 64] = O[h][d];
+                    for (int d = 0; d < ND; d++) *field(h, d) = O[h][d];
                     mlx[h][qw][lane] = float4v{m[h], l[h], started[h] ? 1.f : 0.f, 0.f};
                 }
             }
@@ -460,7 +484,6 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             if (kg == 0) {
 #pragma unroll
                 for (int h = 0; h < G; h++) {
-                    const float4v* st = reinterpret_cast<const float4v*>(stage_of(h >> 1, h & 1)) + qw * ND * 64 + lane;
                     const float4v ml = mlx[h][qw][lane];
                     const float m1 = ml[0], l1 = ml[1];
                     const bool s1 = ml[2] != 0.f;
@@ -468,7 +491,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                     const float a0 = started[h] ? fast_exp2(m[h] - M) : 0.f;
                     const float a1 = s1 ? fast_exp2(m1 - M) : 0.f;
 #pragma unroll
-                    for (int d = 0; d < ND; d++) O[h][d] = O[h][d] * a0 + st[d * 64] * a1;
+                    for (int d = 0; d < ND; d++) O[h][d] = O[h][d] * a0 + *field(h, d) * a1;
                     l[h] = l[h] * a0 + l1 * a1;
                     m[h] = (started[h] || s1) ? M : m[h];
                     started[h] = started[h] || s1;
@@ -496,7 +519,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
             for (int d = 0; d < ND; d++) *reinterpret_cast<float4v*>(dst + 16 * d) = O[h][d] * inv;
         } else {
             const uint32_t n_head = n_head_kv * G;
-            float* dst = part + ((size_t(split) * n_tok + row) * n_head + head) * kPartStride;
+            float* dst = part + ((size_t(split) * n_tok + row) * n_head + head) * PS;
 #pragma unroll
             for (int d = 0; d < ND; d++) *reinterpret_cast<float4v*>(dst + 16 * d + 4 * g) = O[h][d];
             // a query that saw no key in this split contributes nothing: report m = -inf-like
@@ -509,7 +532,7 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
 // log-sum-exp merge of attn_combine (shaders/kernels.metal:501-516) over the split records.
 // HD/4 threads per (token, head) record, each owning 4 dims; the loads of 4 splits are in
 // flight at once and folded in online (clamped indices keep them unconditional, masked entries
-// get weight 0). A record is kPartStride floats: o[HD], then m and l.
+// get weight 0). A record is HD + 4 floats: o[HD], then m and l.
 constexpr int kCombineThreads = 256;
 constexpr uint32_t kQBlock = 64;  // queries per prefill workgroup (16 x kQW)
 template <int HD>
@@ -517,18 +540,18 @@ __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
     const float* __restrict__ part, float* __restrict__ out, uint32_t pos, uint32_t n_tok,
     uint32_t n_head, uint32_t q_stride, uint32_t tps) {
     constexpr int TPR = HD / 4;  // threads per record
-    static_assert(HD + 2 <= kPartStride, "record fits");
+    constexpr int PS = HD + 4;   // floats per record
     const uint32_t rec = blockIdx.x * (kCombineThreads / TPR) + threadIdx.x / TPR;
     if (rec >= n_tok * n_head) return;
     const uint32_t row = rec / n_head, h = rec % n_head;
     // The split count of this token's query block, as the prefill kernel enumerates it; blocks
     // of one split wrote their output directly.
     const uint32_t blk_end = min(n_tok, (row / kQBlock + 1) * kQBlock);
-    const uint32_t n_splits = ((pos + blk_end + kBN - 1) / kBN + tps - 1) / tps;
+    const uint32_t n_splits = ((pos + blk_end + kBN<HD> - 1) / kBN<HD> + tps - 1) / tps;
     if (n_splits == 1) return;
     const int d = 4 * (threadIdx.x % TPR);
-    const size_t sstride = size_t(n_tok) * n_head * kPartStride;
-    const float* src = part + size_t(rec) * kPartStride;
+    const size_t sstride = size_t(n_tok) * n_head * PS;
+    const float* src = part + size_t(rec) * PS;
     float M = kNoMax, L = 0.f;
     float4v O = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t s0 = 0; s0 < n_splits; s0 += 4) {
@@ -562,11 +585,12 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                      uint32_t kv_div, uint32_t n_splits, float qscale, hipStream_t stream) {
     static_assert(16 * kQW == kQBlock, "query block size");
-    const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
+    constexpr uint32_t BN = kBN<HD>;
+    const uint32_t max_tiles = (pos + n_tok + BN - 1) / BN;
     const uint32_t tps = (max_tiles + n_splits - 1) / n_splits;  // tiles per split at most
     uint32_t pairs = 0;  // (query block, split) pairs: the kernel's enumeration
     for (uint32_t b = 0; b * kQBlock < n_tok; b++) {
-        const uint32_t nt = (pos + min(n_tok, (b + 1) * kQBlock) + kBN - 1) / kBN;
+        const uint32_t nt = (pos + min(n_tok, (b + 1) * kQBlock) + BN - 1) / BN;
         pairs += (nt + tps - 1) / tps;
     }
     if (uint64_t(pairs) * n_head_kv > 0x7fffffffu) return -1;
@@ -587,24 +611,28 @@ int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float
 
 }  // namespace
 
-uint32_t prefill_unit_heads(uint32_t group) {
-    // At most 3 heads per unit: the 4-head instantiation needs more than the 256 registers two
-    // waves per SIMD leave and spills (measured 163 TFLOP/s at 32 Q / 8 KV heads, C4 shape,
-    // against 600 for 3 heads), so a group of 4 runs as two units of 2.
-    for (uint32_t g = group < 3 ? group : 3; g > 1; g--)
+uint32_t prefill_unit_heads(uint32_t group, uint32_t head_dim) {
+    // At most 3 heads per unit (1 for head_dim 256): more O accumulators than that need more
+    // than the 256 registers two waves per SIMD leave and spill (4 heads of 128 measured 163
+    // TFLOP/s at 32 Q / 8 KV heads, C4 shape, against 600 for 3), so a group of 4 runs as two
+    // units of 2.
+    const uint32_t cap = head_dim == 256 ? 1 : 3;
+    for (uint32_t g = group < cap ? group : cap; g > 1; g--)
         if (group % g == 0) return g;
     return 1;
 }
 
-uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t requested) {
-    const uint32_t max_tiles = (pos + n_tok + kBN - 1) / kBN;
+uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32_t head_dim,
+                        uint32_t requested) {
+    const uint32_t BN = head_dim == 256 ? kBN<256> : kBN<128>;
+    const uint32_t max_tiles = (pos + n_tok + BN - 1) / BN;
     const uint32_t cap = min(max_tiles, kMaxPrefillSplits);
     // (query block, split) workgroups for at most s splits per block (the kernel's enumeration)
     auto workgroups = [&](uint32_t s) {
         const uint32_t tps = (max_tiles + s - 1) / s;
         uint64_t pairs = 0;
         for (uint32_t b = 0; b * kQBlock < n_tok; b++)
-            pairs += ((pos + min(n_tok, (b + 1) * kQBlock) + kBN - 1) / kBN + tps - 1) / tps;
+            pairs += ((pos + min(n_tok, (b + 1) * kQBlock) + BN - 1) / BN + tps - 1) / tps;
         return pairs * n_head_kv;
     };
     uint32_t s = min(requested, cap);
@@ -646,11 +674,17 @@ int launch_prefill_hd(const float* q, const _Float16* k, const _Float16* v, floa
                                        group, 1, qscale, stream);
     // Groups above 3 run as units of gs heads (the largest divisor of the group up to 3), kv_div of
     // them per KV head, each reading that head's K/V.
-    const uint32_t gs = prefill_unit_heads(group), kv_div = group / gs, units = n_head_kv * kv_div;
+    const uint32_t gs = prefill_unit_heads(group, HD), kv_div = group / gs, units = n_head_kv * kv_div;
     switch (gs) {
         case 1: return launch_prefill_g<HD, 1>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
-        case 2: return launch_prefill_g<HD, 2>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
-        case 3: return launch_prefill_g<HD, 3>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+        case 2:
+            if constexpr (HD != 256)
+                return launch_prefill_g<HD, 2>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+            return -2;
+        case 3:
+            if constexpr (HD != 256)
+                return launch_prefill_g<HD, 3>(q, k, v, out, part, pos, n_tok, q_stride, units, kv_div, n_splits, qscale, stream);
+            return -2;
         default: return -2;
     }
 }
@@ -664,6 +698,7 @@ int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* 
     switch (head_dim) {
         case 64: return launch_prefill_hd<64>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, group, n_splits, scale, stream);
         case 128: return launch_prefill_hd<128>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, group, n_splits, scale, stream);
+        case 256: return launch_prefill_hd<256>(q, k, v, out, part, pos, n_tok, q_stride, n_head_kv, group, n_splits, scale, stream);
         default: return -2;
     }
 }

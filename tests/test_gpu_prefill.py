@@ -166,10 +166,9 @@ def test_prefill_rows_equal_decode_steps(dev):
 @pytest.mark.parametrize("n_head,n_head_kv,hd", [(32, 8, 64), (16, 8, 256), (64, 8, 128), (48, 8, 128),
                                                   (40, 8, 128), (16, 2, 64)])
 def test_prefill_head_dims_and_groups(dev, oracle_mod, n_head, n_head_kv, hd):
-    # head_dim 64 (the MFMA kernel), 256 (the generic kernel, token by token) and groups above 3
-    # on the MFMA kernel (units of up to 3 heads): the reference takes these through its flash
-    # prefill (any group, src/metal_backend.mm:360) or its naive kernel
-    # (shaders/kernels.metal:639-702).
+    # head_dim 64 and 256 and groups above 3 on the MFMA kernel (units of up to 3 heads, 1 for
+    # head_dim 256): the reference takes these through its flash prefill (any group,
+    # src/metal_backend.mm:360) or its naive kernel (shaders/kernels.metal:639-702).
     import ingot_attn as ia
     import torch
 
@@ -203,20 +202,21 @@ def test_prefill_group8_split(dev, oracle_mod):
     assert_parity(got, want, "prefill G=8 split")
 
 
-@pytest.mark.parametrize("n_head,n_head_kv,pos,n_tok", [(32, 8, 3000, 512), (24, 8, 0, 512), (16, 2, 1000, 130)])
-def test_prefill_hd64_mfma(dev, oracle_mod, n_head, n_head_kv, pos, n_tok):
-    # head_dim 64 on the MFMA kernel: a long prefix (key split + combine), a chunk from 0 (the
-    # head split), and a ragged chunk with few KV heads.
+@pytest.mark.parametrize("hd,n_head,n_head_kv,pos,n_tok", [
+    (64, 32, 8, 3000, 512), (64, 24, 8, 0, 512), (64, 16, 2, 1000, 130),
+    (256, 16, 8, 3000, 512), (256, 16, 8, 0, 256), (256, 12, 4, 700, 77)])
+def test_prefill_mfma_head_dims(dev, oracle_mod, hd, n_head, n_head_kv, pos, n_tok):
+    # head_dim 64 and 256 on the MFMA kernel: a long prefix (key split + combine), a chunk from 0
+    # (the head split), and a ragged chunk with few KV heads.
     import ingot_attn as ia
 
-    hd = 64
     d = ia.prefill_desc(n_head, n_head_kv, hd, pos, n_tok)
-    print(f"[prefill] hd=64 {n_head}/{n_head_kv} {n_tok}@{pos} splits={ia.prefill_splits(d)}", flush=True)
-    rng = np.random.Generator(np.random.PCG64(7 * n_head + pos))
+    print(f"[prefill] hd={hd} {n_head}/{n_head_kv} {n_tok}@{pos} splits={ia.prefill_splits(d)}", flush=True)
+    rng = np.random.Generator(np.random.PCG64(7 * n_head + pos + hd))
     L = pos + n_tok
     q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
     kb = rng.standard_normal((L, n_head_kv * hd)).astype(np.float16).view(np.uint16)
     vb = rng.standard_normal((L, n_head_kv * hd)).astype(np.float16).view(np.uint16)
     got = _run_prefill(dev, q, kb, vb, n_head, n_head_kv, pos, n_tok, head_dim=hd)
     want = oracle_mod.attn_prefill(q, kb, vb, n_head, n_head_kv, hd, pos, n_tok, threads=16)
-    assert_parity(got, want, f"prefill hd=64 {n_head}/{n_head_kv} {n_tok}@{pos}")
+    assert_parity(got, want, f"prefill hd={hd} {n_head}/{n_head_kv} {n_tok}@{pos}")
