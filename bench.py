@@ -72,7 +72,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", default="all",
-                    help="all | decode | prefill | kvstore | linear | model | probes | copy-probe | one of "
+                    help="all | decode | prefill | kvstore | linear | model | envelope | probes | copy-probe | one of "
                     + ", ".join(list(DECODE) + list(PREFILL) + list(KVSTORE) + list(LINEAR)))
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-graph", action="store_true", help="launch eagerly instead of replaying a HIP graph")
@@ -281,6 +281,54 @@ def cpu_baseline(W, seconds):
                       f"5 calls, {dt1 * 1e3:.1f} ms/call"}
 
 
+# Shapes outside the Llama-3.2-3B headline (the a10 envelope and other group sizes), one size
+# each: (name, n_head, n_head_kv, head_dim, n_keys) for decode, (..., pos, n_tok) for prefill.
+ENVELOPE_DECODE = (("decode-64/8-hd128-4096", 64, 8, 128, 4096),
+                   ("decode-32/8-hd64-4096", 32, 8, 64, 4096),
+                   ("decode-16/8-hd256-4096", 16, 8, 256, 4096))
+ENVELOPE_PREFILL = (("prefill-32/8-hd128-512@3584", 32, 8, 128, 3584, 512),
+                    ("prefill-32/8-hd64-512@3584", 32, 8, 64, 3584, 512),
+                    ("prefill-16/8-hd256-512@3584", 16, 8, 256, 3584, 512))
+
+
+def envelope(torch, ia, steps, warmup, use_graph):
+    """Decode and prefill at other head sizes and group sizes: 16 rotated layer slices of a
+    random f16 cache (K/V from HBM), per-call time, algorithmic bytes or FLOPs."""
+    dev = torch.device("cuda:0")
+    ws = ia.Workspace(dev)
+    n_layer = 16
+    out = {}
+    for name, nh, nkv, hd, L in ENVELOPE_DECODE:
+        kvd = nkv * hd
+        k = torch.randn(n_layer * L, kvd, device=dev).half()
+        v = torch.randn_like(k)
+        q = torch.randn(nh * hd, device=dev)
+        o = torch.empty_like(q)
+        ds = [ia.decode_desc(nh, nkv, hd, L, kv_offset=i * L * kvd) for i in range(n_layer)]
+        sps = time_steps(torch, lambda: [ia.attn_decode(q, k, v, o, d, workspace=ws) for d in ds],
+                         steps, warmup, use_graph) / n_layer
+        nbytes = 2 * L * kvd * 2 + 2 * nh * hd * 4
+        out[name] = {"us_per_call": round(sps * 1e6, 3), "GB/s": round(nbytes / sps / 1e9, 1),
+                     "hbm_frac": round(nbytes / sps / 1e9 / HBM_PEAK_GBS, 4)}
+        del k, v
+        torch.cuda.empty_cache()
+    for name, nh, nkv, hd, pos, nt in ENVELOPE_PREFILL:
+        kvd, nk = nkv * hd, pos + nt
+        k = torch.randn(n_layer * nk, kvd, device=dev).half()
+        v = torch.randn_like(k)
+        q = torch.randn(nt, nh * hd, device=dev)
+        o = torch.empty_like(q)
+        ds = [ia.prefill_desc(nh, nkv, hd, pos, nt, kv_offset=i * nk * kvd) for i in range(n_layer)]
+        sps = time_steps(torch, lambda: [ia.attn_prefill(q, k, v, o, d, workspace=ws) for d in ds],
+                         max(5, steps // 5), warmup, use_graph) / n_layer
+        flops = 4 * hd * nh * (nt * pos + nt * (nt + 1) // 2)
+        out[name] = {"us_per_call": round(sps * 1e6, 2), "TFLOPS": round(flops / sps / 1e12, 1),
+                     "mfma_frac": round(flops / sps / 1e12 / MFMA_F16_PEAK_TFS, 4)}
+        del k, v
+        torch.cuda.empty_cache()
+    return out
+
+
 def probes(torch, W):
     """Achievable peaks on this box, measured the same way as the kernels: a plain streaming
     read of the C3 decode bytes (1024 workgroups, 28 rotated copies so the data comes from HBM)
@@ -451,6 +499,9 @@ def main():
             del b
             torch.cuda.empty_cache()
         res["model"][f"Llama-3.2-3B-{t}"] = entry
+
+    if sel in ("all", "envelope"):
+        res["envelope"] = envelope(torch, ia, args.steps, args.warmup, use_graph)
 
     if sel in ("all", "probes"):
         res["probes"] = probes(torch, W)
