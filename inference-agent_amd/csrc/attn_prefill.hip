@@ -5,14 +5,17 @@
 // steps (src/backend.h:16-20, src/cpu_backend.cpp:51-69) and of the reference's attn_prefill
 // (shaders/kernels.metal:518-633, mask `key <= pos+tok`, line 578), re-designed for CDNA4:
 //
-//   - A workgroup = 8 waves over one KV head and 64 queries: 4 query waves x 2 key groups. A
-//     wave owns 16 queries and ALL G query heads of the group (48 score columns for G = 3);
+//   - Head size HD = 64, 128 or 256 (a template parameter: row bytes, swizzles, k steps).
+//   - A workgroup = 8 waves over one unit (G <= 3 query heads of one KV head; 1 at HD 256) and
+//     64 queries: 4 query waves x 2 key groups. A wave owns 16 queries and the unit's G heads
+//     (48 score columns for G = 3);
 //     the two key groups take alternate key tiles (each with its own double-buffered LDS
 //     stages) and are merged through LDS at the end, which gives 2 waves per SIMD without
 //     splitting the key range across workgroups. Every K/V operand read from LDS feeds G MFMAs
 //     (v_mfma_f32_16x16x32_f16), so the GQA sharing happens at register level, on top of the
 //     workgroup-level sharing of each LDS tile.
-//   - K/V tiles (64 keys) are copied HBM -> LDS with global_load_lds (no VGPRs, no VALU) into a
+//   - K/V tiles (64 keys; 32 at HD 256) are copied HBM -> LDS with buffer_load ... lds (no
+//     VGPRs, no VALU) into a
 //     double buffer: the next tile streams in while the current one is computed. 16-byte
 //     chunks are XOR-swizzled per row so that every LDS read below is bank-conflict free.
 //   - S^T = K Q^T: the A operand is a 16-byte LDS read of a K row, B is Q^T held in registers
