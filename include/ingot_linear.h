@@ -113,12 +113,15 @@ typedef struct IngotProjDesc {
 
 /* A chunk (n_tok > 1) runs the batched linear-layer kernel over the rows of every matrix in one
  * launch, without split-K: x is [n_tok][n_in], out[m] is [n_tok][n_out[m]], prologue
- * INGOT_PROJ_X and epilogue INGOT_PROJ_STORE or INGOT_PROJ_ACCUMULATE only (else
- * INGOT_ATTN_EUNSUPPORTED). Each out[m] equals that of ingot_linear (n_tok, n_splits = 1) on
- * matrix m, bit for bit. It replaces the q/k/v encode_linear calls of a chunk
- * (src/metal_backend.mm:440-442) where the three matrices' row tiles together fill the GPU
- * better than each alone (Llama-3.2-3B at 512 tokens: 160 tiles of 256 rows x 64 tokens against
- * 96 + 32 + 32 in three launches).
+ * INGOT_PROJ_X (else INGOT_ATTN_EUNSUPPORTED). With INGOT_PROJ_STORE or INGOT_PROJ_ACCUMULATE
+ * each out[m] equals that of ingot_linear (n_tok, n_splits = 1) on matrix m, bit for bit. It
+ * replaces the q/k/v encode_linear calls of a chunk (src/metal_backend.mm:440-442) where the
+ * three matrices' row tiles together fill the GPU better than each alone (Llama-3.2-3B at 512
+ * tokens: 160 tiles of 256 rows x 64 tokens against 96 + 32 + 32 in three launches). With
+ * INGOT_PROJ_SILU_GATE (two matrices of equal n_out) out[0] = silu(W[0]·x) * (W[1]·x) per
+ * element, equal bit for bit to ingot_linear on each matrix (n_splits = 1) followed by
+ * ingot_silu_mul; it replaces the gate and up encode_linear calls and encode_silu_mul of a chunk
+ * (src/metal_backend.mm:448-451) with one launch whose tiles hold 128 rows of each matrix.
  *   w       host array of n_mats device pointers to the weight bytes, each 16-byte aligned
  *   x       [n_in] f32 ([n_tok][n_in] for a chunk), 16-byte aligned
  *   norm_w  [n_in] f32 rmsnorm weights, 16-byte aligned (INGOT_PROJ_RMSNORM; else ignored)

@@ -96,8 +96,8 @@ int check_proj(const void* const* w, const float* x, const float* norm_w, const 
     for (uint32_t m = 0; m < d->n_mats; m++)
         if (!w[m] || !aligned16(w[m]) || d->n_out[m] == 0) return INGOT_ATTN_EINVAL;
     if (uint64_t(d->n_in) / elems * bytes > 0x7fffffffull) return INGOT_ATTN_EUNSUPPORTED;
-    if (d->n_tok > 1) {  // a chunk: the batched kernel, no prologue or fused epilogue
-        if (d->prologue != INGOT_PROJ_X || d->epilogue > INGOT_PROJ_ACCUMULATE) return INGOT_ATTN_EUNSUPPORTED;
+    if (d->n_tok > 1) {  // a chunk: the batched kernel, no prologue
+        if (d->prologue != INGOT_PROJ_X) return INGOT_ATTN_EUNSUPPORTED;
         for (uint32_t m = 0; m < d->n_mats; m++)
             if (uint64_t(d->n_tok) * d->n_out[m] > 0xffffffffffffull) return INGOT_ATTN_EINVAL;
     }

@@ -1083,7 +1083,10 @@ struct MmMats {
     uint32_t tile_end[2];
 };
 
-template <int T, bool LW>
+// PAIR: the gate/up projections of the feed-forward block in one launch: a row tile is 128 rows
+// of matrix 0 (gate, waves 0-3) and the same 128 rows of matrix 1 (up, waves 4-7), and the
+// output is silu(gate) * up (unsplit, no accumulate).
+template <int T, bool LW, bool PAIR = false>
 __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const MmMats mats, const float* __restrict__ x,
     uint32_t n_in, uint32_t n_tok, uint32_t row_bytes, uint32_t accumulate,
@@ -1107,16 +1110,18 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     if (L >= total) return;
     const uint32_t split = L % splits, tt = (L / splits) % tiles_m, rt = L / splits / tiles_m;
     // This row tile's matrix (selected without indexing the argument arrays, which would put
-    // them in scratch) and its tile index within that matrix.
-    const uint32_t mat = rt < mats.tile_end[0] ? 0u : rt < mats.tile_end[1] ? 1u : 2u;
+    // them in scratch) and its tile index within that matrix; with PAIR the wave's matrix.
+    constexpr uint32_t RT = PAIR ? kMmRows / 2 : kMmRows;  // rows of one matrix per tile
+    const uint32_t mat = PAIR ? wave / 4 : rt < mats.tile_end[0] ? 0u : rt < mats.tile_end[1] ? 1u : 2u;
     const uint8_t* __restrict__ const W = mat == 0 ? mats.W[0] : mat == 1 ? mats.W[1] : mats.W[2];
-    float* __restrict__ const out = mat == 0 ? mats.out[0] : mat == 1 ? mats.out[1] : mats.out[2];
-    const uint32_t n_out = mat == 0 ? mats.n_out[0] : mat == 1 ? mats.n_out[1] : mats.n_out[2];
-    const uint32_t rtl = rt - (mat == 0 ? 0u : mat == 1 ? mats.tile_end[0] : mats.tile_end[1]);
+    float* __restrict__ const out = PAIR || mat == 0 ? mats.out[0] : mat == 1 ? mats.out[1] : mats.out[2];
+    const uint32_t n_out = PAIR || mat == 0 ? mats.n_out[0] : mat == 1 ? mats.n_out[1] : mats.n_out[2];
+    const uint32_t rtl = PAIR ? rt : rt - (mat == 0 ? 0u : mat == 1 ? mats.tile_end[0] : mats.tile_end[1]);
     const uint32_t kbeg = split * k_per_split;
     const uint32_t steps = (min(n_in, kbeg + k_per_split) - kbeg) / kMmK;
     const uint32_t tok0 = tt * kMmToks;
-    const uint32_t rowbase = rtl * kMmRows + wave * kMmRowsWave;
+    const uint32_t rowbase = rtl * RT + (PAIR ? wave % 4 : wave) * kMmRowsWave;
+    const bool writer = !PAIR || wave < 4;  // the waves that write the output
 
     // x staging: thread t converts 4 consecutive k of token t/8. Loads are unconditional (rows
     // past n_tok read the last token, steps past the split re-read its last step; neither
@@ -1145,7 +1150,8 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         // stage: P steps of 4 MFMAs between barriers.
         constexpr uint32_t KS = Stage<T>::ks, P = KS / kMmK, SB = Stage<T>::bytes;
         constexpr uint32_t PITCH = Stage<T>::pitch, CH = SB / 16;
-        constexpr uint32_t NCH = (kMmRows * CH + 511) / 512;
+        constexpr uint32_t NM = PAIR ? 2 : 1;                // matrices staged per tile
+        constexpr uint32_t NCH = (RT * CH + 511) / 512;      // chunks per thread per matrix
         // x stages of XK elements (NXS per W stage), as large as the LDS left by the W double
         // buffer allows
         constexpr uint32_t XK = T == kQ8_0 ? 64 : (KS < 128 ? KS : 128);
@@ -1159,29 +1165,36 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         static_assert(kMmWaves * kOutStage * 4 <= 2 * kMmRows * PITCH, "output staging fits");
         ost = reinterpret_cast<float*>(wsm);
         const uint32_t nst = steps / P;
-        const uint32_t rows_here = min(n_out - rtl * kMmRows, uint32_t(kMmRows));
-        const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint8_t*>(W + size_t(rtl) * kMmRows * row_bytes), 0, int(rows_here * row_bytes),
-            kBufferFlags);
+        // One descriptor per staged matrix (a load instruction never mixes them: a per-lane
+        // choice would make the compiler loop over the wave's distinct descriptors).
+        const uint32_t rows_here = min(n_out - rtl * RT, RT);
+        __amdgpu_buffer_rsrc_t wrs[NM];
+        for (uint32_t m = 0; m < NM; m++)
+            wrs[m] = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint8_t*>((PAIR ? (m == 0 ? mats.W[0] : mats.W[1]) : W) + size_t(rtl) * RT * row_bytes),
+                0, int(rows_here * row_bytes), kBufferFlags);
         const uint32_t kbyte0 = kbeg / Fmt<T>::blk * Fmt<T>::bytes;
         uint32_t goff[NCH], loff[NCH];
         for (uint32_t i = 0; i < NCH; i++) {
-            const uint32_t c = min(tid + 512 * i, kMmRows * CH - 1);
+            const uint32_t c = min(tid + 512 * i, RT * CH - 1);
             const uint32_t r = c / CH, o = c % CH;
             goff[i] = min(r, rows_here - 1) * row_bytes + kbyte0 + 16 * o;
-            loff[i] = r * PITCH + 16 * o;
+            loff[i] = r * PITCH + 16 * o;  // matrix m's rows follow at m * RT * PITCH
         }
-        u32x4 wr[2][NCH];
+        u32x4 wr[2][NM][NCH];
         auto load_w = [&](int slot, uint32_t j) {
             const uint32_t sb = min(j, nst - 1) * SB;
-            for (uint32_t i = 0; i < NCH; i++)
-                wr[slot][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                            wrs, int(goff[i] + sb), 0, 0));
+            for (uint32_t m = 0; m < NM; m++)
+                for (uint32_t i = 0; i < NCH; i++)
+                    wr[slot][m][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                   wrs[m], int(goff[i] + sb), 0, 0));
         };
         auto store_w = [&](int slot) {
             uint8_t* base = wsm + slot * (kMmRows * PITCH);
-            for (uint32_t i = 0; i < NCH; i++)
-                if (tid + 512 * i < kMmRows * CH) *reinterpret_cast<u32x4*>(base + loff[i]) = wr[slot][i];
+            for (uint32_t m = 0; m < NM; m++)
+                for (uint32_t i = 0; i < NCH; i++)
+                    if (tid + 512 * i < RT * CH)
+                        *reinterpret_cast<u32x4*>(base + m * RT * PITCH + loff[i]) = wr[slot][m][i];
         };
         const uint32_t xk = 4 * (tid % 8);
         const uint32_t xso = 4 * (min(st_tok, x_rows - 1) * n_in + kbeg + xk);
@@ -1368,6 +1381,22 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         if (tid == 0)  // leave the workspace ready for the next call
             __hip_atomic_store(counters + tile * 16, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    if constexpr (PAIR) {
+        // The up waves hand their tiles to the gate waves of the same rows through LDS (16
+        // floats per lane per pass, lane-minor), which form silu(gate) * up as silu_mul_kernel.
+        for (int i = 0; i < 2; i++) {
+            __syncthreads();  // the LDS is free (loop reads, or the previous pass)
+            float* xb = ost + (wave % 4) * (16 * 64) + lane;
+            if (!writer)
+                for (int e = 0; e < 16; e++) xb[e * 64] = acc[i][e];
+            __syncthreads();
+            if (writer)
+                for (int e = 0; e < 16; e++) {
+                    const float g = acc[i][e];
+                    acc[i][e] = g / (1.0f + expf(-g)) * xb[e * 64];
+                }
+        }
+    }
     // Output: out[tok][row] = prev + acc for the wave's 64 tokens x 32 rows. With 16-byte
     // aligned rows the tile is transposed through LDS, 32 tokens at a time, so that each lane
     // loads and stores 16 contiguous bytes (8 lanes per token row: 8 instructions each way
@@ -1392,14 +1421,14 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
             for (int k = 0; k < 4; k++) {
                 const uint32_t tok = tok0 + 32 * i + 8 * k + tr;
                 const float4v v = *reinterpret_cast<const float4v*>(st + (8 * k + tr) * kOutPitch + c4);
-                if (tok < n_tok && row0 < n_out)
+                if (writer && tok < n_tok && row0 < n_out)
                     *reinterpret_cast<float4v*>(out + size_t(tok) * n_out + row0) = prev[i][k] + v;
             }
         }
         return;
     }
     const uint32_t orow = rowbase + n;
-    if (orow < n_out) {
+    if (writer && orow < n_out) {
         float prev[2][16];
         for (int i = 0; i < 2; i++)
             for (int e = 0; e < 16; e++) {
@@ -1416,14 +1445,22 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
 
 // The batched kernel over mats (n_mats matrices; W, out and n_out set) with `splits`-way
 // split-K (partials and counters in the workspace when splits > 1).
+// pair: mats holds (gate, up) with equal n_out and out[0] receives silu(gate) * up (no split,
+// no accumulate).
 template <int T>
 int launch_mm_t(MmMats mats, uint32_t n_mats, const float* x, uint32_t n_in, uint32_t n_tok,
-                uint32_t accumulate, uint32_t splits, void* workspace, hipStream_t stream) {
+                uint32_t accumulate, uint32_t splits, void* workspace, hipStream_t stream,
+                bool pair = false) {
     const uint32_t row_bytes = n_in / Fmt<T>::blk * Fmt<T>::bytes;
     uint32_t tiles_n = 0;
-    for (uint32_t m = 0; m < 3; m++) {
-        if (m < n_mats) tiles_n += (mats.n_out[m] + kMmRows - 1) / kMmRows;
-        if (m < 2) mats.tile_end[m] = tiles_n;
+    if (pair) {
+        if (n_mats != 2 || mats.n_out[0] != mats.n_out[1] || accumulate || splits != 1) return -1;
+        tiles_n = (mats.n_out[0] + kMmRows / 2 - 1) / (kMmRows / 2);
+    } else {
+        for (uint32_t m = 0; m < 3; m++) {
+            if (m < n_mats) tiles_n += (mats.n_out[m] + kMmRows - 1) / kMmRows;
+            if (m < 2) mats.tile_end[m] = tiles_n;
+        }
     }
     const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
     // LDS-staged W when rows split into whole 16-byte stage pieces.
@@ -1440,23 +1477,26 @@ int launch_mm_t(MmMats mats, uint32_t n_mats, const float* x, uint32_t n_in, uin
     auto* part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kLinearCounterBytes)
                             : nullptr;
     const dim3 grid(uint32_t(per_xcd * 8)), block(kMmWaves * 64);
-    if constexpr (Stage<T>::ks != 0) {
-        if (lw) {
-            const size_t lds = size_t(2) * kMmRows * Stage<T>::pitch;
+    auto go = [&](auto lw_c, auto pair_c) {
+        constexpr bool LWc = decltype(lw_c)::value, PAIRc = decltype(pair_c)::value;
+        const size_t lds = LWc ? size_t(2) * kMmRows * Stage<T>::pitch : 0;
+        if (LWc) {
             static const hipError_t attr = hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&linear_matmul_kernel<T, true>),
+                reinterpret_cast<const void*>(&linear_matmul_kernel<T, LWc, PAIRc>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
             if (attr != hipSuccess) return -4;
-            hipLaunchKernelGGL((linear_matmul_kernel<T, true>), grid, block, lds, stream, mats, x,
-                               n_in, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits,
-                               k_per_split, uint32_t(per_xcd), part, counters);
-            return hipGetLastError() == hipSuccess ? 0 : -4;
         }
+        hipLaunchKernelGGL((linear_matmul_kernel<T, LWc, PAIRc>), grid, block, lds, stream, mats, x,
+                           n_in, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits,
+                           k_per_split, uint32_t(per_xcd), part, counters);
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    };
+    using yes = std::true_type;
+    using no = std::false_type;
+    if constexpr (Stage<T>::ks != 0) {
+        if (lw) return pair ? go(yes{}, yes{}) : go(yes{}, no{});
     }
-    hipLaunchKernelGGL((linear_matmul_kernel<T, false>), grid, block, 0, stream, mats, x, n_in,
-                       n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits, k_per_split,
-                       uint32_t(per_xcd), part, counters);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+    return pair ? go(no{}, yes{}) : go(no{}, no{});
 }
 
 template <int T>
@@ -1519,22 +1559,27 @@ int launch_proj(uint32_t type, const void* const* W, const float* x, const float
                 float* const* out, uint32_t n_in, const uint32_t* n_out, uint32_t n_mats,
                 int pro, int epi, float eps, hipStream_t stream, const ProjRope* rope, uint32_t n_tok) {
     if (n_tok > 1) {  // a chunk: the batched kernel over every matrix's rows, no split-K
-        if (pro != kProNone || (epi != kEpiStore && epi != kEpiAccumulate) || rope) return -2;
+        // Epilogues: store, accumulate, or silu(gate) * up over two matrices (one launch with
+        // gate and up rows paired in each tile).
+        const bool pair = epi == kEpiSiluGate;
+        if (pro != kProNone || rope) return -2;
+        if (epi != kEpiStore && epi != kEpiAccumulate && !pair) return -2;
+        if (pair && (n_mats != 2 || n_out[0] != n_out[1])) return -1;
         MmMats mats{};
         for (uint32_t m = 0; m < n_mats; m++) {
             mats.W[m] = static_cast<const uint8_t*>(W[m]);
-            mats.out[m] = out[m];
+            mats.out[m] = pair ? out[0] : out[m];
             mats.n_out[m] = n_out[m];
         }
         const uint32_t acc = epi == kEpiAccumulate ? 1u : 0u;
         switch (type) {
-            case kF32:  return launch_mm_t<kF32>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
-            case kF16:  return launch_mm_t<kF16>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
-            case kBF16: return launch_mm_t<kBF16>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
-            case kQ8_0: return launch_mm_t<kQ8_0>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
-            case kQ4_0: return launch_mm_t<kQ4_0>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
-            case kQ4_1: return launch_mm_t<kQ4_1>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
-            case kQ6_K: return launch_mm_t<kQ6_K>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream);
+            case kF32:  return launch_mm_t<kF32>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream, pair);
+            case kF16:  return launch_mm_t<kF16>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream, pair);
+            case kBF16: return launch_mm_t<kBF16>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream, pair);
+            case kQ8_0: return launch_mm_t<kQ8_0>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream, pair);
+            case kQ4_0: return launch_mm_t<kQ4_0>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream, pair);
+            case kQ4_1: return launch_mm_t<kQ4_1>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream, pair);
+            case kQ6_K: return launch_mm_t<kQ6_K>(mats, n_mats, x, n_in, n_tok, acc, 1, nullptr, stream, pair);
             default:    return -2;
         }
     }

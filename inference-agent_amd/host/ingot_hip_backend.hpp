@@ -62,6 +62,9 @@ public:
     // Tiles (256 rows x 64 tokens, over q, k and v) from which a chunk's q/k/v run as one batched
     // launch instead of three split-K launches; a test sets 0 to force the one-launch path.
     uint32_t qkv_one_launch_min_tiles = 128;
+    // Tiles (128 rows of gate and of up x 64 tokens) from which a chunk's gate/up + silu run as
+    // one batched launch; a test sets 0 to force it.
+    uint32_t ffn_one_launch_min_tiles = 256;
 
     // device_weights: the matrices' `data` are device addresses already (gguf::DeviceWeights);
     // otherwise they are host bytes and are copied to the device here.
@@ -173,6 +176,12 @@ public:
                 const Dev* w[2] = {&L.w_gate, &L.w_up};
                 float* outs[1] = {gate_};
                 proj(w, 2, x_, L.ffn_norm, outs, INGOT_PROJ_RMSNORM, INGOT_PROJ_SILU_GATE, "rmsnorm+gate/up");
+            } else if (L.w_gate.type == L.w_up.type && ffn_one_launch(un, nf)) {
+                // A chunk: rmsnorm, then gate/up + silu(gate)*up in one batched launch.
+                abi(ingot_rmsnorm(x_, L.ffn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
+                const Dev* w[2] = {&L.w_gate, &L.w_up};
+                float* outs[1] = {gate_};
+                proj(w, 2, h_, nullptr, outs, INGOT_PROJ_X, INGOT_PROJ_SILU_GATE, "gate/up+silu", un);
             } else {
                 abi(ingot_rmsnorm(x_, L.ffn_norm, h_, ne, un, m_.rms_eps, stream_), "rmsnorm");
                 linear(L.w_gate, h_, gate_, ne, nf, un, false);
@@ -257,6 +266,11 @@ private:
     bool qkv_one_launch(uint32_t n_tok, uint32_t q_dim, uint32_t kv_dim) const {
         const uint32_t rows = (q_dim + 255) / 256 + 2 * ((kv_dim + 255) / 256);
         return uint64_t(rows) * ((n_tok + 63) / 64) >= qkv_one_launch_min_tiles;
+    }
+    // A chunk's gate/up + silu run as one batched launch (no split-K) once the paired tiles of
+    // 128 + 128 rows x 64 tokens fill the 256 CUs (Llama-3.2-3B: 512 at 512 tokens).
+    bool ffn_one_launch(uint32_t n_tok, uint32_t n_ff) const {
+        return uint64_t((n_ff + 127) / 128) * ((n_tok + 63) / 64) >= ffn_one_launch_min_tiles;
     }
     // One token (or a chunk of n_tok) through 1..3 matrices sharing x (ingot_proj).
     void proj(const Dev* const* w, uint32_t n_mats, const float* x, const float* norm_w, float* const* outs,

@@ -7,9 +7,8 @@ residual add, rmsnorm, gate/up projections, silu_mul, down with the residual add
 rmsnorm of the last token and the logits projection. For one token (decode) the rmsnorm, the
 q/k/v projections, RoPE and the KV store are one `ingot_proj_rope_kv` call, rmsnorm + gate/up +
 silu_mul and the final rmsnorm + logits one `ingot_proj` launch each (identical results, fewer
-launches). Every step is one libingot_attn.so
-call;
-PyTorch only holds device memory and the stream. Errors are the reference's
+launches); for a chunk large enough, q/k/v are one batched launch and gate/up + silu_mul another.
+Every step is one libingot_attn.so call; PyTorch only holds device memory and the stream. Errors are the reference's
 (src/metal_backend.mm:421-424): "… batch size out of range", "context window exceeded",
 "token id out of range".
 """
@@ -34,6 +33,19 @@ def qkv_one_launch(n_tok, q_dim, kv_dim):
     256 tokens 80, where three split launches are faster)."""
     rows = -(-q_dim // 256) + 2 * -(-kv_dim // 256)
     return rows * -(-n_tok // 64) >= QKV_ONE_LAUNCH_MIN_TILES
+
+
+# Tiles (128 rows of gate and of up x 64 tokens) from which a chunk's gate/up + silu run as one
+# batched launch; a test sets 0 to force that path.
+FFN_ONE_LAUNCH_MIN_TILES = 256
+
+
+def ffn_one_launch(n_tok, n_ff):
+    """Whether a chunk's gate and up projections and silu(gate) * up run as one batched launch
+    (ingot_proj with the silu epilogue, no split-K) rather than two ingot_linear calls (each
+    split-K over the CUs when its tiles are few) and ingot_silu_mul: once the paired tiles fill
+    the 256 CUs (Llama-3.2-3B: 512 tiles at 512 tokens, 256 at 256)."""
+    return -(-n_ff // 128) * -(-n_tok // 64) >= FFN_ONE_LAUNCH_MIN_TILES
 
 
 class HipForward:
@@ -137,6 +149,10 @@ class HipForward:
                         ia.proj_desc(L["w_gate"][0], ne, [nf, nf], prologue=ia.PROJ_RMSNORM,
                                      epilogue=ia.PROJ_SILU_GATE, eps=eps),
                         norm_w=L["ffn_norm"])
+            elif L["w_gate"][0] == L["w_up"][0] and ffn_one_launch(n, nf):
+                ia.rmsnorm(self.x, L["ffn_norm"], self.h, ne, n, eps)
+                ia.proj([L["w_gate"][1], L["w_up"][1]], self.h, [self.gate],
+                        ia.proj_desc(L["w_gate"][0], ne, [nf, nf], epilogue=ia.PROJ_SILU_GATE, n_tok=n))
             else:
                 ia.rmsnorm(self.x, L["ffn_norm"], self.h, ne, n, eps)
                 self._lin(L["w_gate"], self.h, self.gate, ne, nf, n)

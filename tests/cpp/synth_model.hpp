@@ -76,8 +76,8 @@ struct Owned {
 
 // A two-layer model (512 wide, 4 Q / 2 KV heads of 128, FFN 1024, 500 tokens) with mixed
 // types and tied Q8_0 embeddings.
-// uniform_qkv: wq, wk and wv all Q4_0 (one batched q/k/v launch is possible); otherwise three
-// different types.
+// uniform_qkv: wq, wk and wv all Q4_0 and w_gate, w_up both Q8_0 (one batched q/k/v launch and
+// one batched gate/up + silu launch are possible); otherwise different types.
 inline ingot::HostModel make_model(Owned& own, unsigned seed, bool uniform_qkv = false) {
     ingot::HostModel m;
     m.n_layer = 2; m.n_embd = 512; m.n_head = 4; m.n_head_kv = 2; m.head_dim = 128;
@@ -104,7 +104,7 @@ inline ingot::HostModel make_model(Owned& own, unsigned seed, bool uniform_qkv =
         L.wv = own.make(uniform_qkv ? 2 : 8, kvd, m.n_embd, s, rng);
         L.wo = own.make(2, m.n_embd, qd, 0.5f / std::sqrt(float(qd)), rng);
         L.w_gate = own.make(8, m.n_ff, m.n_embd, s, rng);
-        L.w_up = own.make(1, m.n_ff, m.n_embd, s, rng);
+        L.w_up = own.make(uniform_qkv ? 8 : 1, m.n_ff, m.n_embd, s, rng);
         L.w_down = own.make(2, m.n_embd, m.n_ff, 0.5f / std::sqrt(float(m.n_ff)), rng);
         m.layers.push_back(L);
     }

@@ -125,13 +125,14 @@ int main() {
             std::fill(vc.begin(), vc.end(), 0);
             ingot::HipBackend b(m2, n_ctx, 48);
             b.qkv_one_launch_min_tiles = 0;
+            b.ffn_one_launch_min_tiles = 0;
             const int n = 40;
             const float* got = b.forward_batch(toks.data(), n, 0);
             for (int p = 0; p < n; p++)
                 oracle_forward(&om2, kc.data(), vc.data(), n_ctx, toks[size_t(p)], p, want.data(), 1, 8);
             double r = rel_l2(got, want.data(), m2.n_vocab);
             char buf[96];
-            std::snprintf(buf, sizeof buf, "one-launch q/k/v prefill 40 tokens: rel-L2 %.3e", r);
+            std::snprintf(buf, sizeof buf, "one-launch q/k/v and gate/up prefill 40 tokens: rel-L2 %.3e", r);
             expect(r <= 5e-3, buf);
             for (int p = n; p < n + 3; p++) {
                 got = b.forward(toks[size_t(p)], p);

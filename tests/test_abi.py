@@ -229,9 +229,10 @@ def test_proj_descriptor_checks(lib):
     assert call(ia.proj_desc("F16", 256, [4], epilogue=2)) == -1
     assert call(ia.proj_desc("F16", 256, [4, 8], epilogue=2)) == -1
     assert call(ia.proj_desc("F16", 256, [4, 4, 4], epilogue=2)) == -1
-    # a chunk takes no rmsnorm prologue and no silu epilogue
+    # a chunk takes no rmsnorm prologue (its silu epilogue runs on the GPU: test_gpu_proj.py);
+    # a mismatched silu pair is rejected for chunks too
     assert call(ia.proj_desc("F16", 256, [4], prologue=1, eps=1e-5, n_tok=5)) == -2
-    assert call(ia.proj_desc("F16", 256, [4, 4], epilogue=2, n_tok=5)) == -2
+    assert call(ia.proj_desc("F16", 256, [4, 8], epilogue=2, n_tok=5)) == -1
 
 
 def test_proj_rope_kv_checks(lib):

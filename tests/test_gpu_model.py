@@ -152,13 +152,17 @@ def test_forward_prefill_then_decode(dev, oracle_mod, types, prefill):
 
 
 @pytest.mark.parametrize("types", ["F16", "Q4_0"])
-def test_forward_prefill_one_launch_qkv(dev, oracle_mod, monkeypatch, types):
-    """The chunk's q/k/v through one batched ingot_proj launch (forced; the real threshold needs
-    a Llama-3.2-3B-sized chunk): logits, the K cache rows it wrote and the decode steps after it
-    against the oracle forward."""
+@pytest.mark.parametrize("which", ["qkv", "ffn", "both"])
+def test_forward_prefill_one_launch_qkv(dev, oracle_mod, monkeypatch, types, which):
+    """The chunk's q/k/v through one batched ingot_proj launch, and/or its gate/up + silu
+    through one (forced; the real thresholds need a Llama-3.2-3B-sized chunk): logits, the K
+    cache rows it wrote and the decode steps after it against the oracle forward."""
     import ingot_forward
 
-    monkeypatch.setattr(ingot_forward, "QKV_ONE_LAUNCH_MIN_TILES", 0)
+    if which in ("qkv", "both"):
+        monkeypatch.setattr(ingot_forward, "QKV_ONE_LAUNCH_MIN_TILES", 0)
+    if which in ("ffn", "both"):
+        monkeypatch.setattr(ingot_forward, "FFN_ONE_LAUNCH_MIN_TILES", 0)
     res, kc_gpu, kc_orc = _run(dev, oracle_mod, types, prefill=45, decode_steps=3, tied=True)
     for what, g, w in res:
         assert np.all(np.isfinite(g))
@@ -171,7 +175,7 @@ def test_forward_prefill_one_launch_qkv(dev, oracle_mod, monkeypatch, types):
 @pytest.mark.parametrize("head_dim,n_head,n_head_kv", [(64, 8, 2), (256, 4, 2), (128, 8, 1)])
 def test_forward_other_shapes(dev, oracle_mod, head_dim, n_head, n_head_kv):
     """The whole forward with head_dim 64 (Llama-3.2-1B's; group 4) and 256, and a group of 8
-    (prefill on the MFMA kernel in units of 4 heads): a chunk, then decode steps."""
+    (prefill on the MFMA kernel in units of 2 heads): a chunk, then decode steps."""
     cfg = dict(CFG, n_head=n_head, n_head_kv=n_head_kv, head_dim=head_dim)
     res, kc_gpu, kc_orc = _run(dev, oracle_mod, "F16", prefill=33, decode_steps=3, tied=True, cfg=cfg)
     for what, g, w in res:

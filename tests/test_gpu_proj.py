@@ -232,3 +232,43 @@ def test_chunk_matrices_one_launch(dev, oracle_mod, t, n_tok, n_in, n_outs, acc)
         base = bases[i][rows] if acc else None
         want = oracle_mod.linear(t, raw, x[rows], n_in, n, out=base, accumulate=acc, f16_path=True)
         _close(got, want, f"{t} chunk {n_tok}x{n_in}x{n} matrix {i}")
+
+
+@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("n_tok,n_in,n_ff", [(512, 3072, 8192), (70, 512, 200), (130, 768, 257)])
+def test_chunk_gate_up_silu(dev, oracle_mod, t, n_tok, n_in, n_ff):
+    """A chunk's gate/up projections with the silu epilogue in one launch (128 rows of each
+    matrix per tile): equal bit for bit to ingot_linear on gate and on up (n_splits = 1) followed
+    by ingot_silu_mul, within the matmul bar of the f16-rounding oracle on sampled rows, and
+    nothing past [n_tok][n_ff] written."""
+    import torch
+    import ingot_attn as ia
+
+    rng = np.random.default_rng(n_tok * 3 + n_ff)
+    x = rng.standard_normal((n_tok, n_in)).astype(np.float32)
+    raws = [gb.random_weights(t, n_ff, n_in, seed=n_in + 11 * i + 5) for i in range(2)]
+    xd = _t(x, dev)
+    wd = [_t(r.reshape(-1), dev) for r in raws]
+    pad = 31
+    out = _t(np.full(n_tok * n_ff + pad, np.nan, np.float32), dev)
+    print(f"[proj] chunk gate/up silu {t} {n_tok}x{n_in}x{n_ff}", flush=True)
+    ia.proj(wd, xd, [out], ia.proj_desc(t, n_in, [n_ff, n_ff], epilogue=ia.PROJ_SILU_GATE, n_tok=n_tok))
+    g = _t(np.zeros(n_tok * n_ff, np.float32), dev)
+    u = _t(np.zeros(n_tok * n_ff, np.float32), dev)
+    ia.linear(wd[0], xd, g, ia.linear_desc(t, n_in, n_ff, n_tok, n_splits=1), use_workspace=False)
+    ia.linear(wd[1], xd, u, ia.linear_desc(t, n_in, n_ff, n_tok, n_splits=1), use_workspace=False)
+    got = out.cpu().numpy()
+    if n_tok * n_ff % 4 == 0:  # ingot_silu_mul takes whole float4s
+        ia.silu_mul(g, u, n_tok * n_ff)
+        torch.cuda.synchronize()
+        assert np.array_equal(got[: n_tok * n_ff], g.cpu().numpy()), f"{t}: != linear + linear + silu_mul"
+    else:
+        torch.cuda.synchronize()
+        gh, uh = g.cpu().numpy().astype(np.float64), u.cpu().numpy().astype(np.float64)
+        _close(got[: n_tok * n_ff], gh / (1.0 + np.exp(-gh)) * uh, f"{t}: vs linear + linear + silu")
+    assert np.all(np.isnan(got[n_tok * n_ff:])), f"{t}: wrote past its rows"
+    rows = sorted({0, 1, n_tok // 2, n_tok - 1})
+    gg = oracle_mod.linear(t, raws[0], x[rows], n_in, n_ff, f16_path=True)
+    uu = oracle_mod.linear(t, raws[1], x[rows], n_in, n_ff, f16_path=True)
+    want = gg / (1.0 + np.exp(-gg)) * uu
+    _close(got[: n_tok * n_ff].reshape(n_tok, n_ff)[rows], want, f"{t} chunk gate/up silu")
