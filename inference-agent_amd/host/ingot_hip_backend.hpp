@@ -113,9 +113,11 @@ public:
         logits_dev_ = alloc_f32(size_t(m.n_vocab));
         tokens_dev_ = static_cast<int32_t*>(alloc_bytes(nb * sizeof(int32_t)));
         logits_.resize(size_t(m.n_vocab));
-        // One linear workspace, sized for the largest call of every projection shape.
+        // One linear workspace, sized for the largest call of every projection shape over every
+        // chunk length (a shorter chunk may split its k ranges over more workgroups).
         for (const Dev& w : {layers_[0].wq, layers_[0].wk, layers_[0].wo, layers_[0].w_gate, layers_[0].w_down})
-            lin_ws_bytes_ = std::max(lin_ws_bytes_, ingot_linear_workspace_size_for(w, uint32_t(n_batch)));
+            for (uint32_t n = 2; n <= uint32_t(n_batch); n++)
+                lin_ws_bytes_ = std::max(lin_ws_bytes_, ingot_linear_workspace_size_for(w, n));
         lin_ws_ = alloc_bytes(lin_ws_bytes_);
         check(hipMemset(lin_ws_, 0, lin_ws_bytes_), "linear workspace clear");
     }
