@@ -83,7 +83,7 @@ def test_decode_ragged_lengths(dev, oracle_mod, L):
     assert_parity(got, want, f"L={L}")
 
 
-@pytest.mark.parametrize("splits", [1, 2, 3, 7, 64, 200, 1024])
+@pytest.mark.parametrize("splits", [1, 2, 3, 7, 33, 48, 64, 200, 1024])
 def test_decode_split_invariance(dev, oracle_mod, splits):
     L = 2000
     q, kb, vb = _inputs(77, H, HKV, L)
