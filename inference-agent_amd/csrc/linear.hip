@@ -1065,13 +1065,27 @@ constexpr int kOutStage = 32 * kOutPitch;
 // per row (a whole number of 16-byte chunks, so lanes load full cache lines), stored at a row
 // pitch that keeps the B-operand reads free of bank conflicts. Q6_K has no entry (its 210-byte
 // blocks do not tile rows into 16-byte pieces of a size that fits): it uses the direct path.
-template <int T> struct Stage { static constexpr uint32_t ks = 0, bytes = 0, pitch = 0; };
-template <> struct Stage<kF32>  { static constexpr uint32_t ks = 32,  bytes = 128, pitch = 144; };
-template <> struct Stage<kF16>  { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 144; };
-template <> struct Stage<kBF16> { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 144; };
-template <> struct Stage<kQ8_0> { static constexpr uint32_t ks = 256, bytes = 272, pitch = 272; };
-template <> struct Stage<kQ4_0> { static constexpr uint32_t ks = 256, bytes = 144, pitch = 144; };
-template <> struct Stage<kQ4_1> { static constexpr uint32_t ks = 256, bytes = 160, pitch = 176; };
+template <int T> struct Stage { static constexpr uint32_t ks = 0, bytes = 0, pitch = 0; static constexpr bool swz = false; };
+template <> struct Stage<kF32>  { static constexpr uint32_t ks = 32,  bytes = 128, pitch = 128; static constexpr bool swz = true; };
+template <> struct Stage<kF16>  { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 128; static constexpr bool swz = true; };
+template <> struct Stage<kBF16> { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 128; static constexpr bool swz = true; };
+template <> struct Stage<kQ8_0> { static constexpr uint32_t ks = 256, bytes = 272, pitch = 272; static constexpr bool swz = false; };
+template <> struct Stage<kQ4_0> { static constexpr uint32_t ks = 256, bytes = 144, pitch = 144; static constexpr bool swz = false; };
+template <> struct Stage<kQ4_1> { static constexpr uint32_t ks = 256, bytes = 160, pitch = 176; static constexpr bool swz = false; };
+
+// 16-byte chunk swizzles of the LDS stages (XOR of the chunk index with a function of the row)
+// so that the 16-row b128 reads and the 2-row (b128) or 4-row (b64) write groups each touch 64
+// distinct banks. 128-byte rows (two rows per 64 banks): rows of one parity take the 8 chunk
+// positions in the order of g3(r >> 1), whose bit 2 alternates between consecutive pairs.
+__device__ __forceinline__ uint32_t g3(uint32_t m) { return ((m & 1) << 2) | ((m >> 1) & 3); }
+__device__ __forceinline__ uint32_t swz128(uint32_t r) { return g3((r >> 1) & 7); }
+// x rows of XK halves: 64 B (four rows per 64 banks), 128 B, 256 B (one row per 64 banks).
+template <uint32_t XK>
+__device__ __forceinline__ uint32_t swz_x(uint32_t r) {
+    if constexpr (XK == 32) return (r >> 2) & 3;
+    else if constexpr (XK == 64) return swz128(r);
+    else return ((r & 3) << 2) | ((r >> 2) & 3);
+}
 
 // Up to three matrices of one type sharing n_in and x (q/k/v of a chunk) in one launch: their
 // row tiles are numbered one after another, matrix m taking tiles [tile_end[m-1], tile_end[m]);
@@ -1156,7 +1170,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         // buffer allows
         constexpr uint32_t XK = T == kQ8_0 ? 64 : (KS < 128 ? KS : 128);
         constexpr uint32_t NXS = KS / XK, PX = XK / kMmK;  // x stages per W stage, steps per x stage
-        constexpr uint32_t XP = XK + 8;    // halves per token row of an x stage (conflict-free A reads)
+        constexpr uint32_t XP = XK;        // halves per token row of an x stage (chunks swizzled)
         constexpr uint32_t XF4 = XK / 32;  // float4 x loads per thread per x stage
         static_assert(KS % XK == 0 && XK % kMmK == 0 && kMmToks * XK == 512 * 4 * XF4, "stage shape");
         static_assert(2 * kMmRows * PITCH + 2 * kMmToks * XP * 2 <= 160 * 1024, "LDS");
@@ -1179,7 +1193,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
             const uint32_t c = min(tid + 512 * i, RT * CH - 1);
             const uint32_t r = c / CH, o = c % CH;
             goff[i] = min(r, rows_here - 1) * row_bytes + kbyte0 + 16 * o;
-            loff[i] = r * PITCH + 16 * o;  // matrix m's rows follow at m * RT * PITCH
+            loff[i] = r * PITCH + 16 * (Stage<T>::swz ? o ^ swz128(r) : o);  // matrix m's rows follow at m * RT * PITCH
         }
         u32x4 wr[2][NM][NCH];
         // Token tile tt walks its stages starting at stage tt * nst / tiles_m and wrapping, so
@@ -1222,7 +1236,8 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                 const half4_ hv = kFragSwap13<T>
                     ? half4_{_Float16(v[0]), _Float16(v[2]), _Float16(v[1]), _Float16(v[3])}
                     : half4_{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
-                *reinterpret_cast<half4_*>(&xst[buf][st_tok * XP + 32 * i + xk]) = hv;
+                const uint32_t ch = (4 * i + (tid % 8) / 2) ^ swz_x<XK>(st_tok);
+                *reinterpret_cast<half4_*>(&xst[buf][st_tok * XP + 8 * ch + 4 * (tid & 1)]) = hv;
             }
         };
 
@@ -1253,13 +1268,26 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                         const uint32_t u = xs_i * PX + v;  // step within the W stage
                         const uint32_t t = j * P + u;
                         Raw<T> r;
-                        load_raw_lds<T>(r, wrow, u * kMmK, h);
+                        if constexpr (Stage<T>::swz) {
+                            const uint32_t sw = swz128(wave * kMmRowsWave + n);
+                            if constexpr (T == kF32) {
+                                for (int s = 0; s < 2; s++)
+                                    for (int e = 0; e < 2; e++)
+                                        r.v[s][e] = *reinterpret_cast<const float4v*>(wrow + 16 * ((8 * u + 4 * s + 2 * h + e) ^ sw));
+                            } else {
+                                for (int s = 0; s < 2; s++)
+                                    r.v[s] = *reinterpret_cast<const std::remove_reference_t<decltype(r.v[0])>*>(wrow + 16 * ((4 * u + 2 * s + h) ^ sw));
+                            }
+                        } else {
+                            load_raw_lds<T>(r, wrow, u * kMmK, h);
+                        }
                         half8 b[2];
                         for (int s = 0; s < 2; s++) b[s] = frag<T>(r, s, kbeg + t * kMmK);
 #pragma unroll
                         for (int s = 0; s < 2; s++) {
                             for (int i = 0; i < 2; i++) {
-                                const half8 a = *reinterpret_cast<const half8*>(&xsb[(32 * i + n) * XP + v * kMmK + 16 * s + 8 * h]);
+                                const uint32_t xr = 32 * i + n;
+                                const half8 a = *reinterpret_cast<const half8*>(&xsb[xr * XP + 8 * ((4 * v + 2 * s + h) ^ swz_x<XK>(xr))]);
                                 acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[s], acc[i], 0, 0, 0);
                             }
                         }
