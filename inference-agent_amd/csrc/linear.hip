@@ -1100,7 +1100,7 @@ struct MmMats {
 // PAIR: the gate/up projections of the feed-forward block in one launch: a row tile is 128 rows
 // of matrix 0 (gate, waves 0-3) and the same 128 rows of matrix 1 (up, waves 4-7), and the
 // output is silu(gate) * up (unsplit, no accumulate).
-template <int T, bool LW, bool PAIR = false>
+template <int T, bool LW, bool PAIR = false, int TT = 1>
 __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const MmMats mats, const float* __restrict__ x,
     uint32_t n_in, uint32_t n_tok, uint32_t row_bytes, uint32_t accumulate,
@@ -1133,8 +1133,16 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const uint32_t rtl = PAIR ? rt : rt - (mat == 0 ? 0u : mat == 1 ? mats.tile_end[0] : mats.tile_end[1]);
     const uint32_t kbeg = split * k_per_split;
     const uint32_t steps = (min(n_in, kbeg + k_per_split) - kbeg) / kMmK;
-    const uint32_t tok0 = tt * kMmToks;
-    const uint32_t rowbase = rtl * RT + (PAIR ? wave % 4 : wave) * kMmRowsWave;
+    // TT token halves of 64 per tile: with TT = 2 a wave covers 64 tokens x 64 rows (NB = 2
+    // row blocks of 32) instead of 64 x 32, so each A operand read from LDS feeds two MFMAs.
+    static_assert(TT == 1 || (TT == 2 && LW), "two token halves on the LDS-staged path only");
+    constexpr uint32_t NB = TT, TM = kMmToks * TT;
+    const uint32_t th = TT == 1 ? 0u : PAIR ? (wave >> 1) & 1 : wave & 1;   // token half
+    const uint32_t rg = TT == 1 ? (PAIR ? wave % 4 : wave) : PAIR ? wave & 1 : wave >> 1;  // row group
+    const uint32_t tok0 = tt * TM;
+    const uint32_t wtok0 = tok0 + 64 * th;  // the wave's first token
+    const uint32_t rowbase = rtl * RT + rg * kMmRowsWave * NB;
+    const uint32_t lrow0 = (PAIR ? mat * RT : 0) + rg * kMmRowsWave * NB;  // its first row in a stage
     const bool writer = !PAIR || wave < 4;  // the waves that write the output
 
     // x staging: thread t converts 4 consecutive k of token t/8. Loads are unconditional (rows
@@ -1143,11 +1151,11 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const uint32_t st_tok = tid / 8, st_k = 4 * (tid % 8);
     // A buffer load (wave-uniform descriptor over the workgroup's token rows, per-lane offset)
     // keeps the compiler from moving these prefetches next to their use.
-    const uint32_t x_rows = min(n_tok - tok0, uint32_t(kMmToks));
+    const uint32_t x_rows = min(n_tok - tok0, TM);
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(x + size_t(tok0) * n_in), 0, int(4 * x_rows * n_in), kBufferFlags);
-    float16v_ acc[2];
-    for (int i = 0; i < 2; i++)
+    float16v_ acc[2 * NB];  // [token block i][row block j] at i * NB + j
+    for (int i = 0; i < 2 * int(NB); i++)
         for (int e = 0; e < 16; e++) acc[i][e] = 0.f;
     // LDS for the output transpose (kOutStage floats per wave): the W buffers once the loop
     // is done (LW), else an array of its own.
@@ -1168,13 +1176,13 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         constexpr uint32_t NCH = (RT * CH + 511) / 512;      // chunks per thread per matrix
         // x stages of XK elements (NXS per W stage), as large as the LDS left by the W double
         // buffer allows
-        constexpr uint32_t XK = T == kQ8_0 ? 64 : (KS < 128 ? KS : 128);
+        constexpr uint32_t XK = T == kQ8_0 || (TT == 2 && T == kQ4_0) ? 64 : (KS < 128 ? KS : 128);
         constexpr uint32_t NXS = KS / XK, PX = XK / kMmK;  // x stages per W stage, steps per x stage
         constexpr uint32_t XP = XK;        // halves per token row of an x stage (chunks swizzled)
         constexpr uint32_t XF4 = XK / 32;  // float4 x loads per thread per x stage
         static_assert(KS % XK == 0 && XK % kMmK == 0 && kMmToks * XK == 512 * 4 * XF4, "stage shape");
-        static_assert(2 * kMmRows * PITCH + 2 * kMmToks * XP * 2 <= 160 * 1024, "LDS");
-        __shared__ __attribute__((aligned(16))) _Float16 xst[2][kMmToks * XP];
+        static_assert(2 * kMmRows * PITCH + 2 * TM * XP * 2 <= 160 * 1024, "LDS");
+        __shared__ __attribute__((aligned(16))) _Float16 xst[2][TM * XP];
         extern __shared__ __attribute__((aligned(16))) uint8_t wsm[];  // [2][kMmRows][PITCH]
         static_assert(kMmWaves * kOutStage * 4 <= 2 * kMmRows * PITCH, "output staging fits");
         ost = reinterpret_cast<float*>(wsm);
@@ -1196,11 +1204,13 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
             loff[i] = r * PITCH + 16 * (Stage<T>::swz ? o ^ swz128(r) : o);  // matrix m's rows follow at m * RT * PITCH
         }
         u32x4 wr[2][NM][NCH];
-        // Token tile tt walks its stages starting at stage tt * nst / tiles_m and wrapping, so
-        // the token tiles that share these rows read different W lines at any one time (all
-        // starting at stage 0, they queued on the same L2 lines: wo F16 27.9 -> 26.9 us, Q8_0
-        // 37.1 -> 34.6 us).
-        const uint32_t rot = uint32_t(__builtin_amdgcn_readfirstlane(int(tt * nst / tiles_m % nst)));
+        // The tile's 128-token group g walks its stages starting at stage g * nst / groups and
+        // wrapping, so the tiles that share these rows read different W lines at any one time
+        // (all starting at stage 0, they queued on the same L2 lines: wo F16 27.9 -> 26.9 us,
+        // Q8_0 37.1 -> 34.6 us). The order depends on the 128-token group, not on the tile
+        // height, so both tile heights sum every output in the same order.
+        const uint32_t groups = (n_tok + 127) / 128;
+        const uint32_t rot = uint32_t(__builtin_amdgcn_readfirstlane(int(tok0 / 128 * nst / groups % nst)));
         auto phys = [&](uint32_t j) { j = min(j, nst - 1) + rot; return j >= nst ? j - nst : j; };
         auto load_w = [&](int slot, uint32_t j) {
             const uint32_t sb = phys(j) * SB;
@@ -1217,27 +1227,33 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                         *reinterpret_cast<u32x4*>(base + m * RT * PITCH + loff[i]) = wr[slot][m][i];
         };
         const uint32_t xk = 4 * (tid % 8);
-        const uint32_t xso = 4 * (min(st_tok, x_rows - 1) * n_in + kbeg + xk);
-        float4v xq[XF4];
+        uint32_t xso[TT];
+        for (uint32_t q = 0; q < TT; q++) xso[q] = 4 * (min(st_tok + 64 * q, x_rows - 1) * n_in + kbeg + xk);
+        float4v xq[TT][XF4];
         const uint32_t nxs = nst * NXS;  // x stages
         auto load_xs = [&](uint32_t j) {  // x stage j of the walk (NXS per W stage)
             j = min(j, nxs - 1);
             const uint32_t kb = (phys(j / NXS) * NXS + j % NXS) * XK;
 #pragma unroll
-            for (uint32_t i = 0; i < XF4; i++)
-                xq[i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                                        xrs, int(xso + 4 * (kb + 32 * i)), 0, 0));
+            for (uint32_t q = 0; q < TT; q++)
+#pragma unroll
+                for (uint32_t i = 0; i < XF4; i++)
+                    xq[q][i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                                               xrs, int(xso[q] + 4 * (kb + 32 * i)), 0, 0));
         };
         auto store_xs = [&](int buf) {
             typedef _Float16 half4_ __attribute__((ext_vector_type(4)));
 #pragma unroll
+            for (uint32_t q = 0; q < TT; q++)
+#pragma unroll
             for (uint32_t i = 0; i < XF4; i++) {
-                const float4v v = xq[i];
+                const float4v v = xq[q][i];
                 const half4_ hv = kFragSwap13<T>
                     ? half4_{_Float16(v[0]), _Float16(v[2]), _Float16(v[1]), _Float16(v[3])}
                     : half4_{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
-                const uint32_t ch = (4 * i + (tid % 8) / 2) ^ swz_x<XK>(st_tok);
-                *reinterpret_cast<half4_*>(&xst[buf][st_tok * XP + 8 * ch + 4 * (tid & 1)]) = hv;
+                const uint32_t xr = st_tok + 64 * q;
+                const uint32_t ch = (4 * i + (tid % 8) / 2) ^ swz_x<XK>(xr);
+                *reinterpret_cast<half4_*>(&xst[buf][xr * XP + 8 * ch + 4 * (tid & 1)]) = hv;
             }
         };
 
@@ -1254,7 +1270,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
             for (uint32_t jj = 0; jj < 2; jj++) {
                 const uint32_t j = j0 + jj;
                 if (j >= nst) break;
-                const uint8_t* wrow = wsm + jj * (kMmRows * PITCH) + (wave * kMmRowsWave + n) * PITCH;
+                const uint8_t* wrow = wsm + jj * (kMmRows * PITCH) + (lrow0 + n) * PITCH;
                 load_w(jj, j + 2);  // this slot's stage j is already in LDS
                 // Issue the prefetch here: left to the scheduler, these loads sink below the
                 // stage's MFMAs and the next stage waits for them.
@@ -1267,28 +1283,34 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                     for (uint32_t v = 0; v < PX; v++) {
                         const uint32_t u = xs_i * PX + v;  // step within the W stage
                         const uint32_t t = j * P + u;
-                        Raw<T> r;
-                        if constexpr (Stage<T>::swz) {
-                            const uint32_t sw = swz128(wave * kMmRowsWave + n);
-                            if constexpr (T == kF32) {
-                                for (int s = 0; s < 2; s++)
-                                    for (int e = 0; e < 2; e++)
-                                        r.v[s][e] = *reinterpret_cast<const float4v*>(wrow + 16 * ((8 * u + 4 * s + 2 * h + e) ^ sw));
+                        half8 b[NB][2];
+#pragma unroll
+                        for (uint32_t jb = 0; jb < NB; jb++) {
+                            const uint8_t* wr_j = wrow + 32 * jb * PITCH;
+                            Raw<T> r;
+                            if constexpr (Stage<T>::swz) {
+                                const uint32_t sw = swz128(lrow0 + 32 * jb + n);
+                                if constexpr (T == kF32) {
+                                    for (int s = 0; s < 2; s++)
+                                        for (int e = 0; e < 2; e++)
+                                            r.v[s][e] = *reinterpret_cast<const float4v*>(wr_j + 16 * ((8 * u + 4 * s + 2 * h + e) ^ sw));
+                                } else {
+                                    for (int s = 0; s < 2; s++)
+                                        r.v[s] = *reinterpret_cast<const std::remove_reference_t<decltype(r.v[0])>*>(wr_j + 16 * ((4 * u + 2 * s + h) ^ sw));
+                                }
                             } else {
-                                for (int s = 0; s < 2; s++)
-                                    r.v[s] = *reinterpret_cast<const std::remove_reference_t<decltype(r.v[0])>*>(wrow + 16 * ((4 * u + 2 * s + h) ^ sw));
+                                load_raw_lds<T>(r, wr_j, u * kMmK, h);
                             }
-                        } else {
-                            load_raw_lds<T>(r, wrow, u * kMmK, h);
+                            for (int s = 0; s < 2; s++) b[jb][s] = frag<T>(r, s, kbeg + t * kMmK);
                         }
-                        half8 b[2];
-                        for (int s = 0; s < 2; s++) b[s] = frag<T>(r, s, kbeg + t * kMmK);
 #pragma unroll
                         for (int s = 0; s < 2; s++) {
                             for (int i = 0; i < 2; i++) {
-                                const uint32_t xr = 32 * i + n;
+                                const uint32_t xr = 64 * th + 32 * i + n;
                                 const half8 a = *reinterpret_cast<const half8*>(&xsb[xr * XP + 8 * ((4 * v + 2 * s + h) ^ swz_x<XK>(xr))]);
-                                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[s], acc[i], 0, 0, 0);
+#pragma unroll
+                                for (uint32_t jb = 0; jb < NB; jb++)
+                                    acc[i * NB + jb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b[jb][s], acc[i * NB + jb], 0, 0, 0);
                             }
                         }
                     }
@@ -1356,7 +1378,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     }
 
     // D[m][n] of a 32x32 tile: lane holds column n = lane%32, rows 8(e/4) + 4h + e%4.
-    if (splits > 1) {
+    if (TT == 1 && splits > 1) {  // (two token halves are launched unsplit)
         // Publish this split's partial tile (16-byte device-scope stores), count the arrival;
         // the last split of the tile sums the partials in split order and writes the output.
         const uint32_t tile = rt * tiles_m + tt;
@@ -1419,7 +1441,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     if constexpr (PAIR) {
         // The up waves hand their tiles to the gate waves of the same rows through LDS (16
         // floats per lane per pass, lane-minor), which form silu(gate) * up as silu_mul_kernel.
-        for (int i = 0; i < 2; i++) {
+        for (int i = 0; i < 2 * int(NB); i++) {
             __syncthreads();  // the LDS is free (loop reads, or the previous pass)
             float* xb = ost + (wave % 4) * (16 * 64) + lane;
             if (!writer)
@@ -1439,42 +1461,47 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
     const bool vec = ((reinterpret_cast<uintptr_t>(out) | (size_t(n_out) * 4)) & 15) == 0;
     if (vec) {
         const uint32_t tr = lane / 8, c4 = 4 * (lane % 8);  // token row within 8, first row
-        const uint32_t row0 = rowbase + c4;
-        float4v prev[2][4];
-        for (int i = 0; i < 2; i++)
-            for (int k = 0; k < 4; k++) {
-                const uint32_t tok = tok0 + 32 * i + 8 * k + tr;
-                prev[i][k] = accumulate && tok < n_tok && row0 < n_out
-                    ? *reinterpret_cast<const float4v*>(out + size_t(tok) * n_out + row0)
-                    : float4v{0.f, 0.f, 0.f, 0.f};
-            }
         float* st = ost + wave * kOutStage;
-        for (int i = 0; i < 2; i++) {
-            __syncthreads();  // the staging area is free (loop reads, or the previous half)
-            for (int e = 0; e < 16; e++) st[(8 * (e / 4) + 4 * h + e % 4) * kOutPitch + n] = acc[i][e];
-            __syncthreads();
-            for (int k = 0; k < 4; k++) {
-                const uint32_t tok = tok0 + 32 * i + 8 * k + tr;
-                const float4v v = *reinterpret_cast<const float4v*>(st + (8 * k + tr) * kOutPitch + c4);
-                if (writer && tok < n_tok && row0 < n_out)
-                    *reinterpret_cast<float4v*>(out + size_t(tok) * n_out + row0) = prev[i][k] + v;
+        for (uint32_t jb = 0; jb < NB; jb++) {
+            const uint32_t row0 = rowbase + 32 * jb + c4;
+            float4v prev[2][4];
+            for (int i = 0; i < 2; i++)
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t tok = wtok0 + 32 * i + 8 * k + tr;
+                    prev[i][k] = accumulate && tok < n_tok && row0 < n_out
+                        ? *reinterpret_cast<const float4v*>(out + size_t(tok) * n_out + row0)
+                        : float4v{0.f, 0.f, 0.f, 0.f};
+                }
+            for (int i = 0; i < 2; i++) {
+                __syncthreads();  // the staging area is free (loop reads, or the previous pass)
+                for (int e = 0; e < 16; e++)
+                    st[(8 * (e / 4) + 4 * h + e % 4) * kOutPitch + n] = acc[i * NB + jb][e];
+                __syncthreads();
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t tok = wtok0 + 32 * i + 8 * k + tr;
+                    const float4v v = *reinterpret_cast<const float4v*>(st + (8 * k + tr) * kOutPitch + c4);
+                    if (writer && tok < n_tok && row0 < n_out)
+                        *reinterpret_cast<float4v*>(out + size_t(tok) * n_out + row0) = prev[i][k] + v;
+                }
             }
         }
         return;
     }
-    const uint32_t orow = rowbase + n;
-    if (writer && orow < n_out) {
-        float prev[2][16];
-        for (int i = 0; i < 2; i++)
-            for (int e = 0; e < 16; e++) {
-                const uint32_t tok = tok0 + 32 * i + 8 * (e / 4) + 4 * h + e % 4;
-                prev[i][e] = accumulate && tok < n_tok ? out[size_t(tok) * n_out + orow] : 0.f;
-            }
-        for (int i = 0; i < 2; i++)
-            for (int e = 0; e < 16; e++) {
-                const uint32_t tok = tok0 + 32 * i + 8 * (e / 4) + 4 * h + e % 4;
-                if (tok < n_tok) out[size_t(tok) * n_out + orow] = prev[i][e] + acc[i][e];
-            }
+    for (uint32_t jb = 0; jb < NB; jb++) {
+        const uint32_t orow = rowbase + 32 * jb + n;
+        if (writer && orow < n_out) {
+            float prev[2][16];
+            for (int i = 0; i < 2; i++)
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t tok = wtok0 + 32 * i + 8 * (e / 4) + 4 * h + e % 4;
+                    prev[i][e] = accumulate && tok < n_tok ? out[size_t(tok) * n_out + orow] : 0.f;
+                }
+            for (int i = 0; i < 2; i++)
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t tok = wtok0 + 32 * i + 8 * (e / 4) + 4 * h + e % 4;
+                    if (tok < n_tok) out[size_t(tok) * n_out + orow] = prev[i][e] + acc[i * NB + jb][e];
+                }
+        }
     }
 }
 
@@ -1497,10 +1524,19 @@ int launch_mm_t(MmMats mats, uint32_t n_mats, const float* x, uint32_t n_in, uin
             if (m < 2) mats.tile_end[m] = tiles_n;
         }
     }
-    const uint32_t tiles_m = (n_tok + kMmToks - 1) / kMmToks;
     // LDS-staged W when rows split into whole 16-byte stage pieces.
     constexpr uint32_t KS = Stage<T>::ks;
     const bool lw = KS != 0 && row_bytes % 16 == 0 && n_in % (KS != 0 ? KS : 1) == 0;
+    // Tiles of 128 tokens (two halves; waves of 64 x 64: each A operand read from LDS feeds two
+    // MFMAs and each W stage serves twice the tokens) for unsplit calls when they take fewer
+    // rounds of 256 workgroups: a 128-token tile costs ~1.8x a 64-token one (Q4_0 gate/up at
+    // 512 tokens: 256 tiles in 80.0 us against 512 in 89.3; q/k/v at 2048 tokens, 320 tiles in
+    // 2 rounds against 640 in 3: 137.9 against 125.3 us). Q8_0's stages leave no LDS for the
+    // larger x stage.
+    const uint64_t rounds1 = (uint64_t(tiles_n) * ((n_tok + 63) / 64) + 255) / 256;
+    const uint64_t rounds2 = (uint64_t(tiles_n) * ((n_tok + 127) / 128) + 255) / 256;
+    const bool tt2 = T != kQ8_0 && lw && splits == 1 && 9 * rounds2 < 5 * rounds1;
+    const uint32_t tiles_m = (n_tok + kMmToks * (tt2 ? 2 : 1) - 1) / (kMmToks * (tt2 ? 2 : 1));
     const uint32_t gran = lw ? KS : kMmK;
     const uint32_t units = n_in / gran;
     const uint32_t k_per_split = (units + splits - 1) / splits * gran;
@@ -1512,26 +1548,31 @@ int launch_mm_t(MmMats mats, uint32_t n_mats, const float* x, uint32_t n_in, uin
     auto* part = splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kLinearCounterBytes)
                             : nullptr;
     const dim3 grid(uint32_t(per_xcd * 8)), block(kMmWaves * 64);
-    auto go = [&](auto lw_c, auto pair_c) {
+    auto go = [&](auto lw_c, auto pair_c, auto tt_c) {
         constexpr bool LWc = decltype(lw_c)::value, PAIRc = decltype(pair_c)::value;
+        constexpr int TTc = decltype(tt_c)::value;
         const size_t lds = LWc ? size_t(2) * kMmRows * Stage<T>::pitch : 0;
         if (LWc) {
             static const hipError_t attr = hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&linear_matmul_kernel<T, LWc, PAIRc>),
+                reinterpret_cast<const void*>(&linear_matmul_kernel<T, LWc, PAIRc, TTc>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, int(lds));
             if (attr != hipSuccess) return -4;
         }
-        hipLaunchKernelGGL((linear_matmul_kernel<T, LWc, PAIRc>), grid, block, lds, stream, mats, x,
+        hipLaunchKernelGGL((linear_matmul_kernel<T, LWc, PAIRc, TTc>), grid, block, lds, stream, mats, x,
                            n_in, n_tok, row_bytes, accumulate, tiles_n, tiles_m, splits,
                            k_per_split, uint32_t(per_xcd), part, counters);
         return hipGetLastError() == hipSuccess ? 0 : -4;
     };
     using yes = std::true_type;
     using no = std::false_type;
+    using one = std::integral_constant<int, 1>;
+    using two = std::integral_constant<int, 2>;
     if constexpr (Stage<T>::ks != 0) {
-        if (lw) return pair ? go(yes{}, yes{}) : go(yes{}, no{});
+        if constexpr (T != kQ8_0)
+            if (lw && tt2) return pair ? go(yes{}, yes{}, two{}) : go(yes{}, no{}, two{});
+        if (lw) return pair ? go(yes{}, yes{}, one{}) : go(yes{}, no{}, one{});
     }
-    return pair ? go(no{}, yes{}) : go(no{}, no{});
+    return pair ? go(no{}, yes{}, one{}) : go(no{}, no{}, one{});
 }
 
 template <int T>

@@ -197,3 +197,18 @@ def test_requested_splits(dev, oracle_mod, n_splits):
     ref, _ = _run(dev, t, raw, x, n, n, use_workspace=False)
     _close(got, ref, f"n_splits={n_splits} vs unsplit")
     _close(got, oracle_mod.linear(t, raw, x, n, n, f16_path=True), f"n_splits={n_splits}")
+
+
+@pytest.mark.parametrize("t", ["F16", "BF16", "F32", "Q4_0", "Q4_1"])
+@pytest.mark.parametrize("n_out", [2000, 2001])
+def test_batched_128_token_tiles(dev, oracle_mod, t, n_out):
+    """Enough token tiles for two rounds of 64-token tiles take one round of 128-token tiles
+    (waves of 64 tokens x 64 rows); ragged n_tok and n_out (2001: rows not 16-byte aligned, the
+    scalar output path), with the residual add. Matches the f16-path oracle."""
+    n_in, n_tok = 256, 2100  # 8 x 33 tiles of 64 tokens, 8 x 17 of 128
+    raw = gb.random_weights(t, n_out, n_in, seed=55)
+    x = _x(n_tok, n_in, seed=56)
+    base = np.random.default_rng(57).standard_normal(n_tok * n_out).astype(np.float32)
+    got, _ = _run(dev, t, raw, x, n_in, n_out, base=base)
+    want = oracle_mod.linear(t, raw, x, n_in, n_out, f16_path=True) + base.reshape(n_tok, n_out)
+    _close(got, want, f"{t} 128-token tiles")
