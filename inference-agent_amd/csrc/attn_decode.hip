@@ -90,7 +90,7 @@ __device__ __forceinline__ float max_x32(float x) {
     return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-template <int G, int NW>
+template <int G, int NW, bool ROT>
 __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
     float* __restrict__ out, float* __restrict__ part, unsigned int* __restrict__ counters,
@@ -197,32 +197,48 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     };
 
     // Two register buffers alternate (ping-pong), so a prefetch never waits for the step it
-    // follows. The slice's nst workgroup steps (kStride keys each) are walked starting at step
-    // split % nst and wrapping: the slices lie a power-of-two distance apart in the cache (e.g.
-    // 256 keys = 512 KB at 8192 keys and 32 splits), and walked in lockstep from their starts
-    // their concurrent loads pile onto the same memory channels (a load-only probe of this grid
-    // at 8192 keys: 8.54 us in order, 7.39 us rotated). With two steps per slice (4096 keys)
-    // rotation gains nothing, so slices of fewer than three steps keep the plain order. Steps
-    // whose keys all lie past k1 (a wave's part of a short last step) are masked in
-    // compute_step, as the partial ones are.
+    // follows. ROT: the slice's nst workgroup steps (kStride keys each) are walked starting at
+    // step split % nst and wrapping: the slices lie a power-of-two distance apart in the cache
+    // (e.g. 256 keys = 512 KB at 8192 keys and 32 splits), and walked in lockstep from their
+    // starts their concurrent loads pile onto the same memory channels (a load-only probe of
+    // this grid at 8192 keys: 8.54 us in order, 7.39 us rotated). Steps whose keys all lie past
+    // k1 (a wave's part of a short last step) are masked in compute_step, as the partial ones
+    // are. The host launches the in-order walk for slices of fewer than three steps (C3: two),
+    // where rotation gains nothing and its index arithmetic measured ~0.1 us slower.
     constexpr uint32_t kStride = NW * KW;
     const uint32_t nst = (k1 - k0 + kStride - 1) / kStride;
-    const uint32_t rot = nst >= 3 ? split % nst : 0;
-    auto at = [&](uint32_t j) {  // first key of this wave in walk step j (clamped to the last)
-        uint32_t p = min(j, nst - 1) + rot;
-        p = p >= nst ? p - nst : p;
-        return k0 + p * kStride + wave * KW;
-    };
     half8 ka[4], va[4], kb[4], vb[4];
-    load_step(at(0), ka, va);
-    for (uint32_t j = 0; j < nst; j += 2) {
-        load_step(at(j + 1), kb, vb);
-        __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before any of this step's math
-        compute_step(at(j), ka, va);
-        if (j + 1 >= nst) break;
-        load_step(at(j + 2), ka, va);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_step(at(j + 1), kb, vb);
+    if constexpr (ROT) {
+        const uint32_t rot = split % nst;
+        auto at = [&](uint32_t j) {  // first key of this wave in walk step j (clamped to the last)
+            uint32_t p = min(j, nst - 1) + rot;
+            p = p >= nst ? p - nst : p;
+            return k0 + p * kStride + wave * KW;
+        };
+        load_step(at(0), ka, va);
+        for (uint32_t j = 0; j < nst; j += 2) {
+            load_step(at(j + 1), kb, vb);
+            __builtin_amdgcn_sched_barrier(0);  // issue the prefetch before any of this step's math
+            compute_step(at(j), ka, va);
+            if (j + 1 >= nst) break;
+            load_step(at(j + 2), ka, va);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_step(at(j + 1), kb, vb);
+        }
+    } else {  // in order
+        uint32_t base = k0 + wave * KW;
+        load_step(base, ka, va);
+        while (base < k1) {
+            load_step(base + kStride, kb, vb);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_step(base, ka, va);
+            base += kStride;
+            if (base >= k1) break;
+            load_step(base + kStride, ka, va);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_step(base, kb, vb);
+            base += kStride;
+        }
     }
 
     // Publish the wave's partials: lane group r holds dims 8c..8c+7 of its key rows; all four
@@ -322,8 +338,12 @@ template <int G, int NW>
 void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
               const _Float16* v, float* out, float* part, unsigned int* counters, uint32_t n_keys,
               uint32_t per, uint32_t n_splits, uint32_t n_head_kv, float qscale) {
-    hipLaunchKernelGGL((attn_decode_kernel<G, NW>), dim3(n_blocks), dim3(64 * NW), 0, stream, q, k,
-                       v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale);
+    if ((per + 16 * NW - 1) / (16 * NW) >= 3)  // workgroup steps per slice
+        hipLaunchKernelGGL((attn_decode_kernel<G, NW, true>), dim3(n_blocks), dim3(64 * NW), 0, stream, q,
+                           k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale);
+    else
+        hipLaunchKernelGGL((attn_decode_kernel<G, NW, false>), dim3(n_blocks), dim3(64 * NW), 0, stream, q,
+                           k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale);
 }
 
 constexpr int kNW = 4;
