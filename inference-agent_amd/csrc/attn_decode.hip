@@ -338,7 +338,7 @@ template <int G, int NW>
 void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
               const _Float16* v, float* out, float* part, unsigned int* counters, uint32_t n_keys,
               uint32_t per, uint32_t n_splits, uint32_t n_head_kv, float qscale) {
-    if ((per + 16 * NW - 1) / (16 * NW) >= 3)  // workgroup steps per slice
+    if (n_splits > 1 && (per + 16 * NW - 1) / (16 * NW) >= 3)  // several slices of 3+ steps
         hipLaunchKernelGGL((attn_decode_kernel<G, NW, true>), dim3(n_blocks), dim3(64 * NW), 0, stream, q,
                            k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale);
     else
