@@ -28,78 +28,45 @@
 // partials of o (no cross-lane reduction) and its (m, l) in LDS; after one barrier, wave h (h < G)
 // alone merges head h of the workgroup, stores the head's record (o[128], m, l) with 16-byte
 // device-scope stores, waits for them, and bumps the head's completion counter. The last slice to
-// arrive for a head merges that head's n_splits records: lane (half, j) loads 16-byte chunk j of
-// the records of splits half, half + 2, ...; lane t loads (m, l) of split t, the wave reduces the
-// maximum, each lane computes its split's weight once, and the weights reach the chunk owners
-// through LDS. The three heads of a group thus merge in parallel, in three different waves, with
-// no workgroup barrier after the counter. Device-scope (sc1) accesses make the records visible
-// across XCDs without an L2 writeback or invalidate, whatever the workgroup placement.
+// arrive for a head merges that head's n_splits records (decode_merge.h): lane (half, j) loads
+// 16-byte chunk j of the records of splits half, half + 2, ...; lane t loads (m, l) of split t,
+// the wave reduces the maximum, each lane computes its split's weight once, and the weights reach
+// the chunk owners through LDS. The three heads of a group thus merge in parallel, in three
+// different waves, with no workgroup barrier after the counter. The hand-off is correct whatever
+// the workgroup placement (device-scope accesses throughout).
 //
 // MFMA 16x16x32 f16 register layouts (wave64, lane l, i = l%16, g = l/16):
 //   A (16 x 32): lane holds A[i][8g + e], e = 0..7;  B (32 x 16): lane holds B[8g + e][i];
 //   D (16 x 16): lane holds D[4g + j][i], j = 0..3.
 //
-// Record layout (workspace, after the counters): [head][split][kPartStride] with o[128]
-// (unnormalized, relative to m), m (base 2), l — the reference's part[...][130] record
-// (AD_STRIDE, shaders/kernels.metal:291) with stride 132.
+// Record layout (workspace, after the counters): one region of kDecodeHeadRecordBytes per query
+// head, [split][528 bytes]: o[128] (unnormalized, relative to m), then m (base 2) and l — the
+// reference's part[...][130] record (AD_STRIDE, shaders/kernels.metal:291).
 #include "attn_common.h"
 #include "attn_internal.h"
+#include "decode_merge.h"
 
 namespace ingot {
 
 namespace {
 
-constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw, 32-bit format)
-constexpr int kScDevice = 16;             // buffer cache-policy bits: sc1 = device scope
-
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float row16_max(float x) {
-    x = fmaxf(x, dpp<0xB1>(x));
-    x = fmaxf(x, dpp<0x4E>(x));
-    x = fmaxf(x, dpp<0x141>(x));
-    x = fmaxf(x, dpp<0x140>(x));
-    return x;
-}
+using handoff::max_x16;
+using handoff::max_x32;
+using handoff::row16_max;
 
 __device__ __forceinline__ float lane0(float x) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
 }
 
-// With both operands equal to x, the two results of v_permlane16_swap are {x_l, x_(l^16)} and
-// those of v_permlane32_swap {x_l, x_(l^32)} (gfx950 lane-swap instructions).
-__device__ __forceinline__ float sum_x16(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float sum_x32(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float max_x16(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float max_x32(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 template <int G, int NW, bool ROT>
 __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
-    float* __restrict__ out, float* __restrict__ part, unsigned int* __restrict__ counters,
+    float* __restrict__ out, char* __restrict__ recs, unsigned int* __restrict__ counters,
     uint32_t n_keys, uint32_t keys_per_split, uint32_t n_splits, uint32_t n_head_kv,
     float qscale) {
     static_assert(G <= NW, "one tail wave per query head of the group");
     static_assert(kMaxDecodeSplits <= 64, "one lane per split in the merge");
     constexpr int KW = 16;  // keys per wave step
-    constexpr int ITER = int(kMaxDecodeSplits) / 2;
     __shared__ __attribute__((aligned(16))) float lds_o[NW][4][G][kHeadDim];  // per lane group r
     __shared__ float lds_ml[NW][G][2];
     __shared__ __attribute__((aligned(16))) float lds_p[NW][KW][4];  // p[key][head] per wave
@@ -280,87 +247,42 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         return;
     }
 
-    // This head's record for this split: 16-byte device-scope stores, awaited before the count.
-    const uint32_t rec_bytes = kPartStride * 4;
-    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        part, 0, uint32_t(n_head_kv * G * n_splits * rec_bytes), kBufferFlags);
-    const int rec0 = int(head * n_splits * rec_bytes);  // byte offset of split 0's record
-    if (lane < 32)
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O), prs,
-                                               rec0 + int(split * rec_bytes) + 16 * j, 0, kScDevice);
-    if (lane == 0)
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(M), __float_as_uint(L)}, prs,
-                                              rec0 + int(split * rec_bytes) + 512, 0, kScDevice);
-    __builtin_amdgcn_s_waitcnt(0);  // the records have reached device scope
-
-    // Ordering of the hand-off without a release/acquire pair: the records above are device-scope
-    // (write-through) stores and the wait above returns only once memory has acknowledged them,
-    // so they are in memory before the counter is incremented; the last arriver's record loads
-    // below are device-scope loads, which do not take a clean L2 line and so read them from
-    // memory. An agent-scope acq_rel increment would in addition write back and invalidate the
-    // whole L2 around the atomic (buffer_wbl2 / buffer_inv sc1): measured 8.0 -> 17.9 us at C3.
+    // The split hand-off (decode_merge.h): store this head's record, count it in, and the last
+    // slice to arrive merges the head's records.
+    const __amdgpu_buffer_rsrc_t rs = handoff::head_region(recs, uint32_t(head));
     unsigned int* counter = counters + head * kCounterStride;
-    unsigned prev = 0;
-    if (lane == 0) prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    prev = __builtin_amdgcn_readfirstlane(prev);
-    if (prev != n_splits - 1) return;
-
-    // Last arriver for this head: merge the n_splits records. Loads are unconditional from
-    // clamped split indices so they are all in flight at once; splits past n_splits get weight 0.
-    const int half = lane >> 5;
-    float4v os[ITER];
-#pragma unroll
-    for (int i = 0; i < ITER; i++) {
-        const uint32_t sp = min(uint32_t(half + 2 * i), n_splits - 1);
-        os[i] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                                prs, rec0 + int(sp * rec_bytes) + 16 * j, 0, kScDevice));
-    }
-    const uint32_t st = min(uint32_t(lane), n_splits - 1);
-    const u32x2 ml = __builtin_amdgcn_raw_buffer_load_b64(prs, rec0 + int(st * rec_bytes) + 512, 0, kScDevice);
-    const float m_s = uint32_t(lane) < n_splits ? __uint_as_float(ml[0]) : kNoMax;
-    const float Mt = max_x32(max_x16(row16_max(m_s)));
-    const float w = fast_exp2(m_s - Mt);  // 0 for lanes past n_splits
-    const float Lt = sum_x32(sum_x16(row16_sum(w * __uint_as_float(ml[1]))));
-    lds_w[h][lane] = w;
-    __builtin_amdgcn_wave_barrier();
-    float4v Ot = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < ITER; i++) Ot += os[i] * lds_w[h][half + 2 * i];
-#pragma unroll
-    for (int e = 0; e < 4; e++) Ot[e] = sum_x32(Ot[e]);
-    if (lane < 32)
-        *reinterpret_cast<float4v*>(out + head * kHeadDim + 4 * j) = Ot * (Lt > 0.f ? 1.f / Lt : 0.f);
-    if (lane == 0)  // leave the workspace ready for the next call
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (handoff::store_and_arrive<kHeadDim>(rs, counter, split, O, M, L, lane) != n_splits - 1) return;
+    handoff::merge_records<kHeadDim, int(kMaxDecodeSplits)>(rs, counter, n_splits, lane, lds_w[h],
+                                                           out + head * kHeadDim);
 }
 
 template <int G, int NW>
 void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
-              const _Float16* v, float* out, float* part, unsigned int* counters, uint32_t n_keys,
+              const _Float16* v, float* out, char* recs, unsigned int* counters, uint32_t n_keys,
               uint32_t per, uint32_t n_splits, uint32_t n_head_kv, float qscale) {
     if (n_splits > 1 && (per + 16 * NW - 1) / (16 * NW) >= 3)  // several slices of 3+ steps
         hipLaunchKernelGGL((attn_decode_kernel<G, NW, true>), dim3(n_blocks), dim3(64 * NW), 0, stream, q,
-                           k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale);
+                           k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale);
     else
         hipLaunchKernelGGL((attn_decode_kernel<G, NW, false>), dim3(n_blocks), dim3(64 * NW), 0, stream, q,
-                           k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale);
+                           k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale);
 }
 
 constexpr int kNW = 4;
 
 }  // namespace
 
-int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, float* out, char* recs,
                        unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
                        uint32_t group, float scale, hipStream_t stream) {
     const uint32_t per = (n_keys + n_splits - 1) / n_splits;
     const uint32_t blocks = n_splits * n_head_kv;
     const float qscale = scale * kLog2e;
     switch (group) {
-        case 1: launch_g<1, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 2: launch_g<2, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 3: launch_g<3, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 4: launch_g<4, kNW>(blocks, stream, q, k, v, out, part, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 1: launch_g<1, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 2: launch_g<2, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 3: launch_g<3, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+        case 4: launch_g<4, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -4;

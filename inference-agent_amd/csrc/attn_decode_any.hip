@@ -8,10 +8,8 @@
 // a workgroup serves G query heads of one KV head (a "unit"); groups larger than the
 // instantiated G are served by several units per KV head (each streams the KV head once).
 //
-// Grid: one dimension. Workgroups 0 .. n_splits*n_units-1 are the key walkers: workgroup b serves
-// unit b % n_units and key slice b / n_units. With several slices, n_units*G merging workgroups
-// follow them, one per query head. The hardware hands workgroup b to XCD b % 8, so with a unit
-// count that is a multiple of 8 all walkers of a unit and the mergers of its heads share one XCD.
+// Grid: one dimension of n_splits * n_units workgroups: workgroup b serves unit b % n_units and
+// key slice b / n_units.
 //
 // Key walkers (4 wave64s; a wave step covers 16 keys and serves all G query heads from each K/V
 // row it reads):
@@ -26,198 +24,44 @@
 //   - K/V come through buffer loads whose descriptors cover exactly the slice (rows past its end
 //     read as zero and are masked), two register buffers alternating: the next step's loads are
 //     in flight while a step is computed.
-//   - The 4 waves merge through LDS; with one slice wave h writes head h's output, else it
-//     stores head h's record: o[HD] as plain floats, then, once those stores are acknowledged,
-//     the (m, l) chunk {m, kFlag, l, kFlag}. A visible flag therefore means a complete o, and
-//     m and l each share an 8-byte (single-copy atomic) pair with a flag.
-//
-// Mergers (4 waves, one query head; wave w owns dims [w*HD/4, (w+1)*HD/4)): wave 0 polls the
-// (m, l) chunks of all slices, sleeping between polls, and clears their flags once all are set
-// (so the next call starts from cleared flags without any epoch); then every wave loads its
-// quarter of each slice's o (4 loads per lane at most) and merges with the log-sum-exp rule in a
-// fixed lane order (deterministic). Merging one head per workgroup keeps each CU's record traffic
-// small: a CU pulls ~51 B/clk from L2, so 3 heads x 32 records through one CU took ~1.5 us.
-// Mergers have the highest workgroup indices: workgroups are dispatched in index order, so when a
-// merger runs every walker has been dispatched and finishes without waiting on anything. The
-// wait is bounded; if it ever ran out the output would be NaN rather than a hang.
-//
-// Where records live. A walker on the XCD its unit is expected on (b % 8, unit count a multiple
-// of 8) stores its record with plain stores: the lines stay dirty in that XCD's L2, where the
-// merger's device-scope loads find them (~0.3 us one way; a device-scope load takes a line dirty
-// in its own L2 and fetches any other from memory). A walker anywhere else writes through to
-// memory with device-scope stores, where a merger on any XCD finds them. The flag says which
-// (kFlagNear / kFlag): a merger that is not on its expected XCD refuses near records (NaN
-// output) rather than read their o lines from memory. Dirty lines do not outlive a call: the
-// kernel's end-of-dispatch release writes L2 back, so a later call's device-scope loads cannot
-// hit a stale dirty line left by a near walker of an earlier call.
+//   - The 4 waves merge through LDS; with one slice wave h writes head h's output. With several,
+//     wave w handles heads w, w + 4 of the unit: it stores the head's record, waits for it to
+//     reach device scope and counts it in on the head's counter; the slice that arrives last
+//     merges the head's records (decode_merge.h). Nothing waits for another workgroup, and
+//     nothing depends on which XCD a workgroup runs on or on the order of dispatch.
 //
 // MFMA 16x16x32 f16 register layouts (wave64, lane l, i = l%16, g = l/16):
 //   A (16 x 32): lane holds A[i][8g + e], e = 0..7;  B (32 x 16): lane holds B[8g + e][i];
 //   D (16 x 16): lane holds D[4g + j][i], j = 0..3.
 //
-// Workspace: the first kCounterBytes hold the tuned kernel's counters (unused here); then one region of
-// kDecodeHeadRecordBytes per query head holding the records [split][HD/4 + 1 chunks of 16 B]:
-// o[HD] (f32), then {m, flag, l, flag} — the reference's part[...][130] record (o, m, l;
-// AD_STRIDE at shaders/kernels.metal:291). Every flag a call sets is cleared by that call's
-// merger, and o is only read after its slice's flag was seen, so data left by earlier calls (any
-// head_dim or split count) is never taken for the current call's.
+// Workspace: the first kCounterBytes hold one counter per query head (kCounterStride words apart);
+// then one region of kDecodeHeadRecordBytes per query head holding the records
+// [split][HD*4 + 16 B]: o[HD], then {m, l} — the reference's part[...][130] record (o, m, l;
+// AD_STRIDE at shaders/kernels.metal:291).
 #include "attn_common.h"
 #include "attn_internal.h"
+#include "decode_merge.h"
 
 namespace ingot {
 
 namespace {
 
 constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw, 32-bit format)
-constexpr int kScDevice = 16;             // buffer cache-policy bits: sc1 = device scope
 constexpr int kNW = 4;                    // waves per workgroup
 constexpr int kKW = 16;                   // keys per wave step
-constexpr uint32_t kSpinLimit = 1u << 16; // polls before giving up (~16 ms; a real wait is < 50)
-constexpr unsigned kFlag = 0x7E57AB1Eu;    // record complete, written through to memory
-constexpr unsigned kFlagNear = 0x7E57AB1Fu;  // record complete, left in the walker's XCD's L2
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float row16_max(float x) {
-    x = fmaxf(x, dpp<0xB1>(x));
-    x = fmaxf(x, dpp<0x4E>(x));
-    x = fmaxf(x, dpp<0x141>(x));
-    x = fmaxf(x, dpp<0x140>(x));
-    return x;
-}
-
-// Hardware id of the XCD (accelerator complex die) this wave runs on.
-__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15; }
+using handoff::row16_max;
 
 __device__ __forceinline__ float readlane_f(float x, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
 }
 
-// Value of x in lane `src` (any lane pattern), through the LDS crossbar.
-__device__ __forceinline__ float lane_value(float x, uint32_t src) {
-    return __int_as_float(__builtin_amdgcn_ds_bpermute(int(src * 4), __float_as_int(x)));
-}
-
-// With both operands equal to x, v_permlane16_swap yields {x_l, x_(l^16)} and
-// v_permlane32_swap {x_l, x_(l^32)} (gfx950 lane-swap instructions).
-__device__ __forceinline__ float add_x16(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float add_x32(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float max_x16(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float max_x32(float x) {
-    const unsigned u = __float_as_uint(x);
-    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-// Max / sum over all 64 lanes; every lane receives the result.
-__device__ __forceinline__ float wave_max(float x) { return max_x32(max_x16(row16_max(x))); }
-__device__ __forceinline__ float wave_sum(float x) { return add_x32(add_x16(row16_sum(x))); }
-
-// A record chunk: plain store (the line stays dirty in this XCD's L2) or device-scope store
-// (written through to memory).
-__device__ __forceinline__ void store_record(u32x4 v, __amdgpu_buffer_rsrc_t rs, int off, bool near) {
-    if (near) __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, 0);
-    else __builtin_amdgcn_raw_buffer_store_b128(v, rs, off, 0, kScDevice);
-}
-
-// The merging workgroup of one query head (see the file comment).
-// `near`: this merger runs on the XCD its unit's walkers are expected on. A record marked near
-// lives dirty in that XCD's L2, so only a near merger can read it; a merger elsewhere that sees
-// such a flag (its line was evicted, the o lines need not have been) rejects the call with NaN
-// instead of reading o from memory. Under the hardware's round-robin dispatch walkers and
-// mergers are all near or all far, so this only guards against another dispatch order.
-template <int HD>
-__device__ void merge_head(char* __restrict__ recs, float* __restrict__ out, uint32_t head,
-                           uint32_t n_splits, bool near, int lane, int wave) {
-    constexpr int CPW = HD / 16;     // 16-byte o chunks in a wave's quarter of one record
-    constexpr int SPI = 64 / CPW;    // splits per load instruction
-    constexpr int MAXS = HD > 128 ? int(kMaxDecodeSplits) / 2 : int(kMaxDecodeSplits);
-    constexpr int NLO = (MAXS + SPI - 1) / SPI;  // o loads per lane, at most
-    constexpr uint32_t rec_bytes = decode_record_bytes(HD);
-    __shared__ float lds_m[64], lds_l[64];
-    __shared__ unsigned lds_ok;
-
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        recs + size_t(head) * kDecodeHeadRecordBytes, 0, uint32_t(kDecodeHeadRecordBytes), kBufferFlags);
-    if (wave == 0) {
-        const int ml_off = int(lane * rec_bytes) + HD * 4;
-        bool ok = uint32_t(lane) >= n_splits, stray = false;
-        u32x4 ml = {0u, 0u, 0u, 0u};
-        uint32_t spins = 0;
-        for (;;) {
-            if (!ok) {
-                ml = __builtin_amdgcn_raw_buffer_load_b128(rs, ml_off, 0, kScDevice);
-                const bool far_flag = ml[1] == kFlag && ml[3] == kFlag;
-                const bool near_flag = ml[1] == kFlagNear && ml[3] == kFlagNear;
-                ok = far_flag || near_flag;
-                stray |= near_flag && !near;
-            }
-            const uint64_t missing = __builtin_amdgcn_ballot_w64(!ok);
-            if (missing == 0 || ++spins >= kSpinLimit) break;
-            // Long sleeps while most slices are still walking, short ones near the end.
-            if (__builtin_popcountll(missing) > 2) __builtin_amdgcn_s_sleep(8);
-            else __builtin_amdgcn_s_sleep(1);
-        }
-        // Clear the flags for the next call (every walker of this call has stored its record).
-        if (uint32_t(lane) < n_splits)
-            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, rs, ml_off, 0, kScDevice);
-        lds_m[lane] = __uint_as_float(ml[0]);
-        lds_l[lane] = __uint_as_float(ml[2]);
-        const bool strays = __builtin_amdgcn_ballot_w64(stray) != 0;
-        if (lane == 0) lds_ok = spins < kSpinLimit && !strays;
-    }
-    __syncthreads();
-    const bool have = uint32_t(lane) < n_splits;
-    const float m_s = have ? lds_m[lane] : kNoMax;
-    const float Mt = wave_max(m_s);
-    const float w_s = fast_exp2(m_s - Mt);  // 0 for lanes past n_splits
-    const float Lt = wave_sum(have ? w_s * lds_l[lane] : 0.f);
-
-    // Lane (c, sg): chunk c of the wave's quarter, splits sg, sg + SPI, ...
-    const int c = lane % CPW, sg = lane / CPW;
-    const int chunk = wave * CPW + c;
-    u32x4 ov[NLO];
-#pragma unroll
-    for (int i = 0; i < NLO; i++) {
-        const uint32_t sp = sg + SPI * i;
-        ov[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, int(min(sp, n_splits - 1) * rec_bytes) + 16 * chunk,
-                                                      0, kScDevice);
-    }
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int i = 0; i < NLO; i++) {
-        const uint32_t sp = sg + SPI * i;
-        const float w = lane_value(w_s, sp < n_splits ? sp : 63u);  // 0 past n_splits
-        acc += __builtin_bit_cast(float4v, ov[i]) * w;
-    }
-    // Sum over the split groups (lanes c + CPW*k) in a fixed order.
-#pragma unroll
-    for (int e = 0; e < 4; e++) {
-        float a = acc[e];
-        if constexpr (SPI >= 16) a += dpp<0x124>(a);  // row_ror:4
-        if constexpr (SPI >= 8) a += dpp<0x128>(a);   // row_ror:8
-        if constexpr (SPI >= 4) a = add_x16(a);
-        acc[e] = add_x32(a);
-    }
-    const float inv = !lds_ok ? __uint_as_float(0x7FC00000u) : (Lt > 0.f ? 1.f / Lt : 0.f);
-    if (sg == 0) *reinterpret_cast<float4v*>(out + size_t(head) * HD + 4 * chunk) = acc * inv;
-}
-
 template <int HD, int G>
 __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
-    float* __restrict__ out, char* __restrict__ recs, uint32_t n_keys,
+    float* __restrict__ out, char* __restrict__ recs, unsigned int* __restrict__ counters, uint32_t n_keys,
     uint32_t keys_per_split, uint32_t n_splits, uint32_t n_units, uint32_t n_sub, uint32_t kv_dim,
     uint32_t group, float qscale) {
     static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim 64, 128 or 256");
@@ -232,17 +76,10 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t n_walk = n_splits * n_units;
-    if (blockIdx.x >= n_walk) {
-        const uint32_t m = blockIdx.x - n_walk, unit = m % n_units, h = m / n_units;
-        const bool near = (n_units & 7) == 0 && xcc_id() == (blockIdx.x & 7);
-        merge_head<HD>(recs, out, (unit / n_sub) * group + (unit % n_sub) * G + h, n_splits, near, lane, wave);
-        return;
-    }
-
     __shared__ __attribute__((aligned(16))) float lds_o[kNW][KPL][G][HD];
     __shared__ float lds_ml[kNW][G][2];
     __shared__ __attribute__((aligned(16))) float lds_p[kNW][kKW][GP];
+    __shared__ float lds_w[kNW][64];  // split weights of the head a wave merges
 
     const int ki = lane & 15, kg = lane >> 4;         // MFMA lane coordinates
     const int vc = lane % CPR, vr = lane / CPR;       // V chunk and key sub-row of the lane
@@ -402,12 +239,10 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
     }
     __syncthreads();
 
-    const bool near = (n_units & 7) == 0 && xcc_id() == (blockIdx.x & 7);
-    constexpr uint32_t rec_bytes = decode_record_bytes(HD);
     for (int h = wave; h < G; h += kNW) {
-        // Merge the workgroup's waves for head h; lane < OL owns dims 4*lane .. 4*lane+3.
-        const bool act = lane < OL;
-        const int d0 = act ? 4 * lane : 0;
+        // Merge the workgroup's waves for head h; lane l owns dims 4c..4c+3, c = l % OL (the lane
+        // layout of the hand-off; lanes with the same c compute the same values).
+        const int d0 = 4 * (lane % OL);
         float M = kNoMax;
 #pragma unroll
         for (int w = 0; w < kNW; w++) M = fmaxf(M, lds_ml[w][h][0]);
@@ -423,40 +258,39 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
             O += s4 * wt;
         }
         const uint32_t head = head0 + h;
+        float* dst = out + size_t(head) * HD;
         if (!multi) {
-            if (act) *reinterpret_cast<float4v*>(out + size_t(head) * HD + d0) = O * (L > 0.f ? 1.f / L : 0.f);
+            if (lane < OL) *reinterpret_cast<float4v*>(dst + d0) = O * (L > 0.f ? 1.f / L : 0.f);
             continue;
         }
-        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            recs + size_t(head) * kDecodeHeadRecordBytes, 0, uint32_t(kDecodeHeadRecordBytes), kBufferFlags);
-        const int my = int(split * rec_bytes);
-        if (act) store_record(__builtin_bit_cast(u32x4, O), rs, my + 4 * d0, near);
-        // The flag goes out only once o is acknowledged (in L2, or in memory when written
-        // through), so a merger that sees it reads a complete o.
-        __builtin_amdgcn_s_waitcnt(0);
-        const unsigned flag = near ? kFlagNear : kFlag;
-        if (lane == 0) store_record(u32x4{__float_as_uint(M), flag, __float_as_uint(L), flag}, rs, my + HD * 4, near);
+        // The split hand-off (decode_merge.h): store this head's record, count it in, and the
+        // last slice to arrive merges the head's records.
+        const __amdgpu_buffer_rsrc_t rs = handoff::head_region(recs, head);
+        unsigned int* counter = counters + head * kCounterStride;
+        if (handoff::store_and_arrive<HD>(rs, counter, split, O, M, L, lane) != n_splits - 1) continue;
+        constexpr int MAXS = HD > 128 ? int(kMaxDecodeSplits) / 2 : int(kMaxDecodeSplits);
+        handoff::merge_records<HD, MAXS>(rs, counter, n_splits, lane, lds_w[wave], dst);
     }
 }
 
 template <int HD, int G>
 void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
-              const _Float16* v, float* out, char* recs, uint32_t n_keys,
+              const _Float16* v, float* out, char* recs, unsigned int* counters, uint32_t n_keys,
               uint32_t per, uint32_t n_splits, uint32_t n_units, uint32_t n_sub,
               uint32_t kv_dim, uint32_t group, float qscale) {
     hipLaunchKernelGGL((attn_decode_kernel<HD, G>), dim3(n_blocks), dim3(64 * kNW), 0, stream, q, k, v,
-                       out, recs, n_keys, per, n_splits, n_units, n_sub, kv_dim, group,
+                       out, recs, counters, n_keys, per, n_splits, n_units, n_sub, kv_dim, group,
                        qscale);
 }
 
 template <int HD>
 int launch_hd(uint32_t gs, uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
-              const _Float16* v, float* out, char* recs, uint32_t n_keys,
+              const _Float16* v, float* out, char* recs, unsigned int* counters, uint32_t n_keys,
               uint32_t per, uint32_t n_splits, uint32_t n_units, uint32_t n_sub,
               uint32_t kv_dim, uint32_t group, float qscale) {
 #define INGOT_DECODE_G(GG)                                                                         \
     case GG:                                                                                       \
-        launch_g<HD, GG>(n_blocks, stream, q, k, v, out, recs, n_keys, per,                       \
+        launch_g<HD, GG>(n_blocks, stream, q, k, v, out, recs, counters, n_keys, per,                       \
                          n_splits, n_units, n_sub, kv_dim, group, qscale);                        \
         return 0;
     switch (gs) {
@@ -508,12 +342,13 @@ namespace {
 }  // namespace
 
 int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, float* out, void* recs,
+                      unsigned int* counters,
                       uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
                       uint32_t head_dim, float scale, hipStream_t stream) {
     const uint32_t per = (n_keys + n_splits - 1) / n_splits;
     const uint32_t gs = decode_unit_heads(group);
     const uint32_t n_sub = group / gs, n_units = n_head_kv * n_sub;
-    const uint64_t blocks = uint64_t(n_splits) * n_units + (n_splits > 1 ? uint64_t(n_units) * gs : 0);
+    const uint64_t blocks = uint64_t(n_splits) * n_units;
     if (blocks > 0x7fffffffu) return -1;
     const uint32_t kv_dim = n_head_kv * head_dim;
     const float qscale = scale * kLog2e;
@@ -521,9 +356,9 @@ int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, floa
     const uint32_t nb = uint32_t(blocks);
     int rc;
     switch (head_dim) {
-        case 64: rc = launch_hd<64>(gs, nb, stream, q, k, v, out, r, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
-        case 128: rc = launch_hd<128>(gs, nb, stream, q, k, v, out, r, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
-        case 256: rc = launch_hd<256>(gs, nb, stream, q, k, v, out, r, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
+        case 64: rc = launch_hd<64>(gs, nb, stream, q, k, v, out, r, counters, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
+        case 128: rc = launch_hd<128>(gs, nb, stream, q, k, v, out, r, counters, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
+        case 256: rc = launch_hd<256>(gs, nb, stream, q, k, v, out, r, counters, n_keys, per, n_splits, n_units, n_sub, kv_dim, group, qscale); break;
         default: return -2;
     }
     if (rc) return rc;
@@ -535,10 +370,10 @@ int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* o
                   uint32_t head_dim, float scale, hipStream_t stream) {
     char* ws = static_cast<char*>(workspace);
     if (head_dim == 128 && group <= 4)
-        return launch_decode_g128(q, k, v, out, reinterpret_cast<float*>(ws + kCounterBytes),
+        return launch_decode_g128(q, k, v, out, ws + kCounterBytes,
                                   reinterpret_cast<unsigned int*>(ws), n_keys, n_splits, n_head_kv, group,
                                   scale, stream);
-    return launch_decode_any(q, k, v, out, ws + kCounterBytes, n_keys, n_splits, n_head_kv, group, head_dim,
+    return launch_decode_any(q, k, v, out, ws + kCounterBytes, reinterpret_cast<unsigned int*>(ws), n_keys, n_splits, n_head_kv, group, head_dim,
                              scale, stream);
 }
 

@@ -11,8 +11,8 @@ namespace ingot {
 // Upper bounds on split counts; they size the workspace.
 constexpr uint32_t kMaxDecodeSplits = 32;
 constexpr uint32_t kMaxPrefillSplits = 16;
-// Completion counters: one per query head, each on its own 256-byte line (no false sharing of
-// the device-scope atomics between heads).
+// Decode hand-off counters (decode_merge.h): one per workgroup unit (at most one per query head),
+// each on its own 256-byte line (no false sharing of the device-scope atomics between units).
 constexpr uint32_t kCounterStride = 64;  // uint32 words
 constexpr size_t kCounterBytes = 65536;  // up to 256 heads
 
@@ -21,10 +21,9 @@ constexpr size_t kCounterBytes = 65536;  // up to 256 heads
 uint32_t decode_splits(uint32_t n_keys, uint32_t head_dim, uint32_t requested);
 uint32_t decode_max_splits(uint32_t head_dim);
 uint32_t decode_unit_heads(uint32_t group);
-// Bytes of one decode split record of the generic kernel: o[head_dim] as f32 and one 16-byte
-// {m, l, flag, flag} chunk; and the fixed region per query head that holds all records of a call
-// (the largest of max splits x record bytes over head_dim 64 / 128 / 256: 32 x 528), which also
-// holds the head_dim-128 kernel's records ([head][split][132] floats).
+// Bytes of one decode split record: o[head_dim] as f32 and one 16-byte chunk holding {m, l}; and
+// the fixed region per query head that holds all records of a call (the largest of max splits x
+// record bytes over head_dim 64 / 128 / 256: 32 x 528). Both decode kernels use this layout.
 constexpr uint32_t decode_record_bytes(uint32_t head_dim) { return head_dim * 4 + 16; }
 constexpr size_t kDecodeHeadRecordBytes = 32 * 528;
 static_assert(kDecodeHeadRecordBytes >= 32 * decode_record_bytes(64) &&
@@ -39,16 +38,16 @@ uint32_t prefill_unit_heads(uint32_t group, uint32_t head_dim);
 constexpr size_t prefill_record_floats(uint32_t head_dim) { return head_dim + 4; }
 
 // Decode attention, dispatched by launch_decode: head_dim 128 with groups 1..4 take the tuned
-// kernel (attn_decode.hip; completion counters in the workspace's first kCounterBytes, records
-// after them), every other shape the generic one (attn_decode_any.hip; records after the first
-// kCounterBytes). Return 0, -1 (grid too large), -2 (shape without a kernel) or -4 (launch failed).
+// kernel (attn_decode.hip), every other shape the generic one (attn_decode_any.hip). Both keep
+// their hand-off counters in the workspace's first kCounterBytes and the records after them. Return 0, -1 (grid too large), -2 (shape without a kernel) or -4 (launch failed).
 int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* out, void* workspace,
                   uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
                   uint32_t head_dim, float scale, hipStream_t stream);
-int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, float* out, char* recs,
                        unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
                        uint32_t group, float scale, hipStream_t stream);
 int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, float* out, void* recs,
+                      unsigned int* counters,
                       uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
                       uint32_t head_dim, float scale, hipStream_t stream);
 // The MFMA prefill kernel (attn_prefill.hip), head_dim 64, 128 or 256.

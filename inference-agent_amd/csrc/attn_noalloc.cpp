@@ -8,9 +8,11 @@
 // process ends. Host code never passes the array's name to a kernel (on the host it is only a
 // stand-in): the first call on a device, with that device current, resolves the device address
 // with hipGetSymbolAddress and keeps it per device, then clears the array with a fill kernel on
-// the caller's stream (the counters and record flags must start at zero; every call leaves them
-// at zero again). After that a call only launches the decode kernels: no hipMalloc, hipFree or
-// allocating library call. All calls on one GPU share that GPU's array, so calls that overlap on
+// the caller's stream. (A __device__ array starts zero-filled when the code object loads, which
+// is what the decode hand-off needs: counters and records at zero, and every call leaves them at
+// zero again. The clear re-establishes that explicitly; under HIP graph capture it is recorded
+// into the graph instead of run, and the array's load-time zeros still hold.) After that a call
+// only launches the decode kernels: no hipMalloc, hipFree or allocating library call. All calls on one GPU share that GPU's array, so calls that overlap on
 // one GPU race: order them on one stream.
 #include <hip/hip_runtime.h>
 
@@ -59,9 +61,11 @@ int device_scratch(void** out, hipStream_t stream) {
 
 extern "C" int ingot_attn_decode_noalloc(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
                                          float* out, const IngotAttnDecodeDesc* d, void* stream) {
-    // Validation happens in ingot_attn_decode; an invalid descriptor has size 0 and is rejected
-    // there with its own code.
-    if (ingot_attn_decode_workspace_size(d) > kScratchBytes) return INGOT_ATTN_EWORKSPACE;
+    // Validate before the scratch is claimed: an invalid descriptor has size 0, and
+    // ingot_attn_decode then rejects it with its own code without touching the device.
+    const size_t need = ingot_attn_decode_workspace_size(d);
+    if (need == 0) return ingot_attn_decode(q, k_cache, v_cache, out, nullptr, 0, d, stream);
+    if (need > kScratchBytes) return INGOT_ATTN_EWORKSPACE;
     void* ws = nullptr;
     const int rc = device_scratch(&ws, static_cast<hipStream_t>(stream));
     if (rc) return rc;

@@ -116,7 +116,7 @@ def test_decode_layer_offset(dev, oracle_mod):
 
 
 def test_decode_repeated_calls_reuse_workspace(dev, oracle_mod):
-    # Split records of earlier calls stay in the workspace; only the current call's tags match.
+    # Every call leaves its counters and records at zero, so the next one starts clean.
     for i, L in enumerate((4096, 700, 4096, 65)):
         q, kb, vb = _inputs(300 + i, H, HKV, L)
         got = _run_decode(dev, q, kb, vb, H, HKV, L)
@@ -159,7 +159,7 @@ def test_decode_split_invariance_head_dims(dev, oracle_mod, hd, splits):
 
 def test_decode_epochs_across_many_calls(dev, oracle_mod):
     # One workspace, 24 calls whose split counts go up and down: a record slot that an earlier
-    # call wrote (with an older tag) must never be taken for the current call's.
+    # call wrote must never be taken for the current call's (each merger zeroes what it read).
     import ingot_attn as ia
 
     ws = ia.Workspace(dev)
@@ -171,6 +171,57 @@ def test_decode_epochs_across_many_calls(dev, oracle_mod):
         got = _run_decode(dev, q, kb, vb, H, HKV, L, n_splits=splits, workspace=ws)
         want = oracle_mod.attn_decode(q, kb, vb, H, HKV, HD, L, threads=8)
         assert_parity(got, want, f"call {i} L={L} splits={splits}")
+
+
+def _counters_all_zero(ws):
+    import torch
+
+    torch.cuda.synchronize()
+    return int(torch.count_nonzero(ws.buf[:65536]).item()) == 0
+
+
+def test_decode_handoff_alternating_shapes_one_workspace(dev, oracle_mod):
+    # Both decode kernels (tuned: head_dim 128, group <= 4; generic: the rest) on one workspace,
+    # head_dims and split counts alternating: records that earlier calls left behind are never
+    # taken for the current call's, and every call leaves its completion counters at zero.
+    import ingot_attn as ia
+
+    ws = ia.Workspace(dev)
+    ws.get(1 << 21)
+    shapes = [(24, 8, 128), (32, 8, 64), (16, 8, 256), (64, 8, 128), (12, 2, 64), (24, 8, 128),
+              (40, 8, 128), (16, 8, 256), (32, 8, 64)]
+    rng = np.random.Generator(np.random.PCG64(77))
+    for i in range(27):
+        n_head, n_head_kv, hd = shapes[i % len(shapes)]
+        L = int(rng.integers(150, 5000))
+        splits = int(rng.choice([0, 0, 2, 3, 9, 16, 32]))
+        q, kb, vb = _inputs(4000 + i, n_head, n_head_kv, L, hd=hd)
+        got = _run_decode(dev, q, kb, vb, n_head, n_head_kv, L, n_splits=splits, hd=hd, workspace=ws)
+        want = oracle_mod.attn_decode(q, kb, vb, n_head, n_head_kv, hd, L, threads=8)
+        assert_parity(got, want, f"call {i} {n_head}/{n_head_kv} hd={hd} L={L} splits={splits}")
+        assert _counters_all_zero(ws), f"call {i}: counters not left at zero"
+
+
+@pytest.mark.parametrize("n_head,n_head_kv,hd", [(24, 8, 128), (32, 8, 64)])
+def test_decode_merge_is_bitwise_reproducible(dev, n_head, n_head_kv, hd):
+    # Which key slice merges depends on the order the slices finish in; the merge sums the
+    # records in split order whichever it is, so repeated calls are bit-identical.
+    import torch
+    import ingot_attn as ia
+
+    L = 4096
+    q, kb, vb = _inputs(61, n_head, n_head_kv, L, hd=hd)
+    qd, kd, vd = _t(q, dev), _t(kb.view(np.int16), dev), _t(vb.view(np.int16), dev)
+    desc = ia.decode_desc(n_head, n_head_kv, hd, L)
+    outs = []
+    for _ in range(16):
+        out = torch.empty(n_head * hd, dtype=torch.float32, device=dev)
+        ia.attn_decode(qd, kd, vd, out, desc)
+        outs.append(out)
+    torch.cuda.synchronize()
+    ref = outs[0].cpu().numpy().view(np.uint32)
+    for o in outs[1:]:
+        assert np.array_equal(o.cpu().numpy().view(np.uint32), ref)
 
 
 def test_decode_closed_forms(dev):

@@ -39,7 +39,7 @@ def _case(dev, seed, n_head, n_head_kv, hd, L):
     return q, kb, vb, t(q), t(kb.view(np.int16)), t(vb.view(np.int16))
 
 
-@pytest.mark.parametrize("shape", [(24, 8, 128), (32, 8, 64)])
+@pytest.mark.parametrize("shape", [(24, 8, 128), (32, 8, 64), (16, 8, 256), (64, 8, 128)])
 def test_noalloc_matches_workspace_entry_point(dev, oracle_mod, shape):
     import torch
     import ingot_attn as ia
@@ -69,3 +69,23 @@ def test_noalloc_rejects_more_heads_than_the_scratch_holds(dev):
     assert lib.ingot_attn_decode_noalloc(p, p, p, p, ctypes.byref(big), None) == -3
     small_one_split = ia.decode_desc(128, 8, 128, 100)  # one split: counters only, fits
     assert lib.ingot_attn_decode_workspace_size(ctypes.byref(small_one_split)) <= 65536 + 64 * 16896
+
+
+def test_noalloc_accepts_many_heads_with_one_split(dev, oracle_mod):
+    # 128 query heads are more than the scratch's record regions hold, but a one-split call
+    # needs no records: the no-allocation entry point takes it and matches ingot_attn_decode.
+    import torch
+    import ingot_attn as ia
+
+    L = 100
+    q, kb, vb, qd, kd, vd = _case(dev, 5, 128, 8, 128, L)
+    desc = ia.decode_desc(128, 8, 128, L)
+    assert ia.load_library().ingot_attn_decode_splits(ctypes.byref(desc)) == 1
+    got = torch.full((128 * 128,), float("nan"), device=dev)
+    ia.attn_decode_noalloc(qd, kd, vd, got, desc)
+    ref = torch.full_like(got, float("nan"))
+    ia.attn_decode(qd, kd, vd, ref, desc, workspace=ia.Workspace(dev))
+    torch.cuda.synchronize()
+    g, r = got.cpu().numpy(), ref.cpu().numpy()
+    assert np.array_equal(g.view(np.uint32), r.view(np.uint32))
+    assert_parity(g, oracle_mod.attn_decode(q, kb, vb, 128, 8, 128, L, threads=8), "noalloc 128 heads")
