@@ -219,7 +219,7 @@ size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d) {
     if (check_prefill(d)) return 0;
     const uint32_t splits = prefill_split_count(d);
     const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head *
-                                          ingot::prefill_record_floats(d->head_dim) * sizeof(float) : 0;
+                                          ingot::prefill_record_bytes(d->head_dim) : 0;
     // The prefill records follow the decode record regions of the same heads, so a workspace
     // shared by decode and prefill calls never holds prefill data where decode tags are read.
     return prefill_part_offset(d->n_head) + parts;
@@ -259,7 +259,7 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const uint32_t splits = prefill_split_count(d);
-    auto* part = reinterpret_cast<float*>(static_cast<char*>(workspace) + prefill_part_offset(d->n_head));
+    char* part = static_cast<char*>(workspace) + prefill_part_offset(d->n_head);
     const int lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
                                           d->n_head / d->n_head_kv, d->head_dim, splits, d->scale, st);
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED

@@ -31,11 +31,12 @@ static_assert(kDecodeHeadRecordBytes >= 32 * decode_record_bytes(64) &&
               kDecodeHeadRecordBytes >= 16 * decode_record_bytes(256), "decode record region");
 // Prefill: split count (n_units = workgroup units: KV heads x group / prefill_unit_heads) and
 // the query heads one MFMA-prefill unit serves (a divisor of the group: at most 3, 1 for
-// head_dim 256). A split record is head_dim + 4 floats.
+// head_dim 256). A split record is o[head_dim] normalized (o / l) as f16, then {m, l} as f32 in a
+// 16-byte chunk.
 uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_units, uint32_t head_dim,
                         uint32_t requested);
 uint32_t prefill_unit_heads(uint32_t group, uint32_t head_dim);
-constexpr size_t prefill_record_floats(uint32_t head_dim) { return head_dim + 4; }
+constexpr size_t prefill_record_bytes(uint32_t head_dim) { return head_dim * 2 + 16; }
 
 // Decode attention, dispatched by launch_decode: head_dim 128 with groups 1..4 take the tuned
 // kernel (attn_decode.hip), every other shape the generic one (attn_decode_any.hip). Both keep
@@ -51,7 +52,7 @@ int launch_decode_any(const float* q, const _Float16* k, const _Float16* v, floa
                       uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
                       uint32_t head_dim, float scale, hipStream_t stream);
 // The MFMA prefill kernel (attn_prefill.hip), head_dim 64, 128 or 256.
-int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, char* part,
                    uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                    uint32_t group, uint32_t head_dim, uint32_t n_splits, float scale,
                    hipStream_t stream);

@@ -89,11 +89,11 @@ template <int HD, int G, int QW, int KG>
 __global__ __launch_bounds__(64 * QW * KG) __attribute__((amdgpu_waves_per_eu(2)))
 void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict__ K,
                          const _Float16* __restrict__ V, float* __restrict__ out,
-                         float* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
+                         char* __restrict__ part, uint32_t pos, uint32_t n_tok, uint32_t q_stride,
                          uint32_t n_head_kv, uint32_t kv_div, uint32_t tps, float qscale) {
     constexpr int BN = kBN<HD>, RB = kRowBytes<HD>, CPR = kChunks<HD>, TB = kTileBytes<HD>, SB = kStageBytes<HD>;
     constexpr int HALVES = BN / 32;  // 32-key halves per tile
-    constexpr int PS = HD + 4;       // floats per split record: o[HD], m, l (16-byte aligned)
+    constexpr int PB = HD * 2 + 16;  // bytes per split record: o[HD] / l as f16, then {m, l, 0, 0}
     constexpr int NIT = TB / 1024;  // 1 KB copy instructions per K (or V) tile
     constexpr int RPI = 1024 / RB;  // rows per copy instruction
     constexpr int KS = HD / 32;     // 32-wide k steps of a score MFMA chain
@@ -501,49 +501,66 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
                 }
             }
         }
-        if (kg == 1) return;
     }
+    const bool owner = kg == 0;  // the waves holding the workgroup's merged O (wave-uniform)
 
     // Row sums: the 4 lane groups g hold partial sums of the same query (same m).
+    if (owner) {
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        l[h] += __shfl_xor(l[h], 16);
-        l[h] += __shfl_xor(l[h], 32);
+        for (int h = 0; h < G; h++) {
+            l[h] += __shfl_xor(l[h], 16);
+            l[h] += __shfl_xor(l[h], 32);
+        }
     }
     const uint32_t row = q0 + li;
-    if (row >= n_tok) return;
+    const bool live = row < n_tok;
+    if (n_splits == 1) {  // the whole key range: write the output
+        if (!owner || !live) return;
 #pragma unroll
-    for (int h = 0; h < G; h++) {
-        const uint32_t head = kvh * G + h;
-        if (n_splits == 1) {
+        for (int h = 0; h < G; h++) {
+            const uint32_t head = kvh * G + h;
             const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
             float* dst = out + size_t(row) * q_stride + size_t(head) * HD + 4 * g;
 #pragma unroll
             for (int d = 0; d < ND; d++) *reinterpret_cast<float4v*>(dst + 16 * d) = O[h][d] * inv;
-        } else {
-            const uint32_t n_head = n_head_kv * G;
-            float* dst = part + ((size_t(split) * n_tok + row) * n_head + head) * PS;
-#pragma unroll
-            for (int d = 0; d < ND; d++) *reinterpret_cast<float4v*>(dst + 16 * d + 4 * g) = O[h][d];
-            // a query that saw no key in this split contributes nothing: report m = -inf-like
-            if (g == 0) *reinterpret_cast<float4v*>(dst + HD) = float4v{started[h] ? m[h] : kNoMax, l[h], 0.f, 0.f};
         }
+        return;
+    }
+
+    // A key split: its record per (query, head) is o / l rounded to f16 (each output element
+    // becomes a weighted mean of the splits' values, so the rounding is relative to the output:
+    // ~2^-12), then (m, l) as f32; a query that saw no key in this split reports m = -inf-like
+    // and l = 0. attn_prefill_combine merges the records. (Merging them in this kernel, by the
+    // last split of each query block to finish, measured slower: C4 50.7 us against 38.3.)
+    if (!owner || !live) return;
+    const uint32_t n_head = n_head_kv * G;
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        char* dst = part + ((size_t(split) * n_tok + row) * n_head + kvh * G + h) * PB;
+        const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
+#pragma unroll
+        for (int d = 0; d < ND; d++) {
+            const float4v v = O[h][d] * inv;
+            *reinterpret_cast<half4*>(dst + 2 * (16 * d + 4 * g)) =
+                half4{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+        }
+        if (g == 0) *reinterpret_cast<float4v*>(dst + 2 * HD) = float4v{started[h] ? m[h] : kNoMax, l[h], 0.f, 0.f};
     }
 }
 
 // out[tok][h][d] = sum_s o_s[d] 2^(m_s - M) / sum_s l_s 2^(m_s - M); 0 if the sum is 0 — the
-// log-sum-exp merge of attn_combine (shaders/kernels.metal:501-516) over the split records.
-// HD/4 threads per (token, head) record, each owning 4 dims; the loads of 4 splits are in
-// flight at once and folded in online (clamped indices keep them unconditional, masked entries
-// get weight 0). A record is HD + 4 floats: o[HD], then m and l.
+// log-sum-exp merge of attn_combine (shaders/kernels.metal:501-516) over the split records, whose
+// o is stored divided by l (so o_s[d] = l_s * rec_s[d]). HD/4 threads per (token, head) record,
+// each owning 4 dims; the loads of 4 splits are in flight at once and folded in online (clamped
+// indices keep them unconditional, masked entries get weight 0).
 constexpr int kCombineThreads = 256;
 constexpr uint32_t kQBlock = 64;  // queries per prefill workgroup (16 x kQW)
 template <int HD>
 __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
-    const float* __restrict__ part, float* __restrict__ out, uint32_t pos, uint32_t n_tok,
+    const char* __restrict__ part, float* __restrict__ out, uint32_t pos, uint32_t n_tok,
     uint32_t n_head, uint32_t q_stride, uint32_t tps) {
-    constexpr int TPR = HD / 4;  // threads per record
-    constexpr int PS = HD + 4;   // floats per record
+    constexpr int TPR = HD / 4;      // threads per record
+    constexpr int PB = HD * 2 + 16;  // bytes per record
     const uint32_t rec = blockIdx.x * (kCombineThreads / TPR) + threadIdx.x / TPR;
     if (rec >= n_tok * n_head) return;
     const uint32_t row = rec / n_head, h = rec % n_head;
@@ -553,26 +570,27 @@ __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
     const uint32_t n_splits = ((pos + blk_end + kBN<HD> - 1) / kBN<HD> + tps - 1) / tps;
     if (n_splits == 1) return;
     const int d = 4 * (threadIdx.x % TPR);
-    const size_t sstride = size_t(n_tok) * n_head * PS;
-    const float* src = part + size_t(rec) * PS;
+    const size_t sstride = size_t(n_tok) * n_head * PB;
+    const char* src = part + size_t(rec) * PB;
     float M = kNoMax, L = 0.f;
     float4v O = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t s0 = 0; s0 < n_splits; s0 += 4) {
         float ms[4], ls[4];
-        float4v os[4];
+        half4 os[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
-            const float* ps = src + min(s0 + u, n_splits - 1) * sstride;
-            ms[u] = s0 + u < n_splits ? ps[HD] : kNoMax;
-            ls[u] = ps[HD + 1];
-            os[u] = *reinterpret_cast<const float4v*>(ps + d);
+            const char* ps = src + min(s0 + u, n_splits - 1) * sstride;
+            const float2 ml = *reinterpret_cast<const float2*>(ps + 2 * HD);
+            ms[u] = s0 + u < n_splits ? ml.x : kNoMax;
+            ls[u] = ml.y;
+            os[u] = *reinterpret_cast<const half4*>(ps + 2 * d);
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const float Mn = fmaxf(M, ms[u]);
-            const float a0 = fast_exp2(M - Mn), a1 = fast_exp2(ms[u] - Mn);
-            L = L * a0 + ls[u] * a1;
-            O = O * a0 + os[u] * a1;
+            const float a0 = fast_exp2(M - Mn), a1 = ls[u] * fast_exp2(ms[u] - Mn);
+            L = L * a0 + a1;
+            O = O * a0 + float4v{float(os[u][0]), float(os[u][1]), float(os[u][2]), float(os[u][3])} * a1;
             M = Mn;
         }
     }
@@ -584,7 +602,7 @@ constexpr int kQW = 4;  // query waves per workgroup (16 queries x G heads each)
 constexpr int kKG = 2;  // key groups per workgroup (alternate tiles, merged through LDS)
 
 template <int HD, int G>
-int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+int launch_prefill_g(const float* q, const _Float16* k, const _Float16* v, float* out, char* part,
                      uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                      uint32_t kv_div, uint32_t n_splits, float qscale, hipStream_t stream) {
     static_assert(16 * kQW == kQBlock, "query block size");
@@ -662,7 +680,7 @@ uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_head_kv, uint32
 namespace {
 
 template <int HD>
-int launch_prefill_hd(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+int launch_prefill_hd(const float* q, const _Float16* k, const _Float16* v, float* out, char* part,
                       uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                       uint32_t group, uint32_t n_splits, float scale, hipStream_t stream) {
     const float qscale = scale * kLog2e;
@@ -694,7 +712,7 @@ int launch_prefill_hd(const float* q, const _Float16* k, const _Float16* v, floa
 
 }  // namespace
 
-int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, float* part,
+int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* out, char* part,
                    uint32_t pos, uint32_t n_tok, uint32_t q_stride, uint32_t n_head_kv,
                    uint32_t group, uint32_t head_dim, uint32_t n_splits, float scale,
                    hipStream_t stream) {
