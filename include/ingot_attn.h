@@ -26,13 +26,16 @@
  *   - Not thread-safe per workspace: two calls that share a workspace must be ordered on one
  *     stream.
  *
- * Supported shapes: head_dim 64, 128 or 256 and any group size n_head / n_head_kv, for decode
- * and prefill (the reference's flash kernels cover head_dim 128 — decode with groups up to 4,
- * src/metal_backend.mm:339, prefill any group, :360 — and its naive kernel every other shape,
- * src/metal_backend.mm:373-382). head_dim 128 runs the tuned decode kernel (groups 1..4,
- * attn_decode.hip), other decode shapes the generic decode kernel; prefill of every head size
- * runs the MFMA kernel (units of up to 3 heads, 1 at head_dim 256). At most 256 query heads (one workspace counter each). Llama-3.2-3B is 24 Q heads /
- * 8 KV heads (group 3); Llama-3.2-1B 32 / 8 with head_dim 64.
+ * Supported shapes: every head_dim from 1 to 1024 and any group size n_head / n_head_kv, for
+ * decode and prefill, as the reference serves them (its flash kernels cover head_dim 128 —
+ * decode with groups up to 4, src/metal_backend.mm:339, prefill any group, :360 — and its naive
+ * kernel every other shape, src/metal_backend.mm:373-382, shaders/kernels.metal:639-702, with
+ * one thread per head dimension, so up to 1024). Here head_dim 128 decode with groups 1..4 runs
+ * the tuned kernel (attn_decode.hip), other head_dim 64/256/128 decode shapes the generic split
+ * kernel, prefill at 64/128/256 the MFMA kernel (units of up to 3 heads, 1 at head_dim 256), and
+ * every other head_dim the fallback kernel (attn_naive.hip, never split). At most 256 query
+ * heads (one workspace counter each). Llama-3.2-3B is 24 Q heads / 8 KV heads (group 3);
+ * Llama-3.2-1B 32 / 8 with head_dim 64.
  */
 #ifndef INGOT_ATTN_H
 #define INGOT_ATTN_H
@@ -46,7 +49,7 @@ extern "C" {
 
 #define INGOT_ATTN_OK 0
 #define INGOT_ATTN_EINVAL (-1)      /* null pointer, zero size, pos/n out of range */
-#define INGOT_ATTN_EUNSUPPORTED (-2) /* head_dim not 64/128/256; n_head > 256;
+#define INGOT_ATTN_EUNSUPPORTED (-2) /* head_dim above 1024; n_head > 256;
                                        linear: weight type or n_in the kernels do not cover */
 #define INGOT_ATTN_EWORKSPACE (-3)  /* workspace smaller than *_workspace_size() */
 #define INGOT_ATTN_EHIP (-4)        /* a HIP runtime call or launch failed */

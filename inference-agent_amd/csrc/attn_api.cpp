@@ -29,26 +29,32 @@ int check_heads(uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim) {
     return INGOT_ATTN_OK;
 }
 
-// Decode: head_dim 64, 128 or 256, any group size.
+// The head sizes of the MFMA kernels; every other head_dim up to kMaxHeadDim runs the fallback
+// kernel of attn_naive.hip (the reference's naive path, src/metal_backend.mm:373-382).
+bool mfma_head_dim(uint32_t hd) { return hd == 64 || hd == 128 || hd == 256; }
+constexpr uint32_t kMaxHeadDim = 1024;
+
+// Decode: any head_dim up to 1024, any group size.
 int check_decode(const IngotAttnDecodeDesc* d) {
     if (!d) return INGOT_ATTN_EINVAL;
     const int rc = check_heads(d->n_head, d->n_head_kv, d->head_dim);
     if (rc) return rc;
-    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return INGOT_ATTN_EUNSUPPORTED;
+    if (d->head_dim > kMaxHeadDim) return INGOT_ATTN_EUNSUPPORTED;
     if (d->n_keys == 0 || d->kv_offset % 8 != 0) return INGOT_ATTN_EINVAL;
     if (!(d->scale > 0.f)) return INGOT_ATTN_EINVAL;
     return INGOT_ATTN_OK;
 }
 
-// Prefill: head_dim 64, 128 or 256, any group size (head_dim 128 on the MFMA kernel).
+// Prefill: any head_dim up to 1024, any group size.
 int check_prefill(const IngotAttnPrefillDesc* d) {
     if (!d) return INGOT_ATTN_EINVAL;
     const int rc = check_heads(d->n_head, d->n_head_kv, d->head_dim);
     if (rc) return rc;
-    if (d->head_dim != 64 && d->head_dim != 128 && d->head_dim != 256) return INGOT_ATTN_EUNSUPPORTED;
+    if (d->head_dim > kMaxHeadDim) return INGOT_ATTN_EUNSUPPORTED;
     if (d->n_tok == 0 || d->kv_offset % 8 != 0) return INGOT_ATTN_EINVAL;
     if (uint64_t(d->pos) + d->n_tok > 0xffffffffull) return INGOT_ATTN_EINVAL;
-    if (d->q_stride < d->n_head * d->head_dim || d->q_stride % 4 != 0) return INGOT_ATTN_EINVAL;
+    if (d->q_stride < d->n_head * d->head_dim) return INGOT_ATTN_EINVAL;
+    if (mfma_head_dim(d->head_dim) && d->q_stride % 4 != 0) return INGOT_ATTN_EINVAL;  // 16-byte q rows
     if (!(d->scale > 0.f)) return INGOT_ATTN_EINVAL;
     return INGOT_ATTN_OK;
 }
@@ -192,13 +198,19 @@ int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w
          : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
 
-uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
-    if (check_decode(d)) return 0;
-    return ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
+// Decode split count (1 for the fallback kernel, which never splits).
+uint32_t decode_split_count(const IngotAttnDecodeDesc* d) {
+    return mfma_head_dim(d->head_dim) ? ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits) : 1u;
 }
 
-// Prefill split count of the MFMA kernel over its workgroup units.
+uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
+    if (check_decode(d)) return 0;
+    return decode_split_count(d);
+}
+
+// Prefill split count of the MFMA kernel over its workgroup units (1 for the fallback kernel).
 uint32_t prefill_split_count(const IngotAttnPrefillDesc* d) {
+    if (!mfma_head_dim(d->head_dim)) return 1;
     const uint32_t group = d->n_head / d->n_head_kv;
     const uint32_t units = d->n_head_kv * (group / ingot::prefill_unit_heads(group, d->head_dim));
     return ingot::prefill_splits(d->pos, d->n_tok, units, d->head_dim, d->n_splits);
@@ -211,7 +223,7 @@ uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
 
 size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
     if (check_decode(d)) return 0;
-    const uint32_t splits = ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
+    const uint32_t splits = decode_split_count(d);
     return kCounterBytes + (splits > 1 ? size_t(d->n_head) * ingot::kDecodeHeadRecordBytes : 0);
 }
 
@@ -235,10 +247,13 @@ int ingot_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
         !aligned16(workspace))
         return INGOT_ATTN_EINVAL;
     if (workspace_bytes < ingot_attn_decode_workspace_size(d)) return INGOT_ATTN_EWORKSPACE;
-    const uint32_t splits = ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits);
+    const uint32_t splits = decode_split_count(d);
     const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
-    const int lrc = ingot::launch_decode(q, k, v, out, workspace, d->n_keys, splits, d->n_head_kv,
+    const int lrc = !mfma_head_dim(d->head_dim)
+        ? ingot::launch_attn_any(q, k, v, out, d->n_keys - 1, 1, d->n_head * d->head_dim, d->n_head, d->n_head_kv,
+                                 d->head_dim, d->scale, static_cast<hipStream_t>(stream))
+        : ingot::launch_decode(q, k, v, out, workspace, d->n_keys, splits, d->n_head_kv,
                                          d->n_head / d->n_head_kv, d->head_dim, d->scale,
                                          static_cast<hipStream_t>(stream));
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
@@ -260,7 +275,10 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
     const hipStream_t st = static_cast<hipStream_t>(stream);
     const uint32_t splits = prefill_split_count(d);
     char* part = static_cast<char*>(workspace) + prefill_part_offset(d->n_head);
-    const int lrc = ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
+    const int lrc = !mfma_head_dim(d->head_dim)
+        ? ingot::launch_attn_any(q, k, v, out, d->pos, d->n_tok, d->q_stride, d->n_head, d->n_head_kv, d->head_dim,
+                                 d->scale, st)
+        : ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
                                           d->n_head / d->n_head_kv, d->head_dim, splits, d->scale, st);
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED
          : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
@@ -322,7 +340,7 @@ const char* ingot_attn_strerror(int code) {
     switch (code) {
         case INGOT_ATTN_OK: return "ok";
         case INGOT_ATTN_EINVAL: return "invalid argument (null/misaligned pointer, zero size or position out of range)";
-        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (attention: head_dim 64/128/256, n_head <= 256; linear: weight type without a kernel or n_in not a multiple of its block)";
+        case INGOT_ATTN_EUNSUPPORTED: return "unsupported shape (attention: head_dim above 1024 or n_head above 256; linear: weight type without a kernel or n_in not a multiple of its block)";
         case INGOT_ATTN_EWORKSPACE: return "workspace smaller than the *_workspace_size() figure";
         case INGOT_ATTN_EHIP: return "HIP launch failed";
         default: return "unknown error";

@@ -57,6 +57,13 @@ int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* 
                    uint32_t group, uint32_t head_dim, uint32_t n_splits, float scale,
                    hipStream_t stream);
 
+// Attention for head sizes without an MFMA kernel (attn_naive.hip): head_dim 1..1024, decode
+// (pos = n_keys - 1, n_tok = 1) and causal prefill. Returns 0, -1 (grid too large), -2 (head_dim
+// above 1024) or -4 (launch failed).
+int launch_attn_any(const float* q, const _Float16* k, const _Float16* v, float* out, uint32_t pos,
+                    uint32_t n_tok, uint32_t q_stride, uint32_t n_head, uint32_t n_head_kv, uint32_t head_dim,
+                    float scale, hipStream_t stream);
+
 // RoPE on q (in place, skipped when q is null) and k; K and V as f16 into the cache rows.
 // Returns 0, -1 (grid too large) or -4 (launch failed).
 int launch_rope_kv_store(float* q, const float* k, const float* v, _Float16* k_cache,

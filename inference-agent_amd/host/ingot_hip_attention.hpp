@@ -46,8 +46,8 @@ public:
         if (c.n_batch < 1) throw std::runtime_error("hip: --batch must be at least 1");
         if (c.n_layer < 1 || c.n_ctx < 1 || c.n_head < 1 || c.n_head_kv < 1)
             throw std::runtime_error("hip: empty model configuration");
-        if (c.head_dim != 64 && c.head_dim != 128 && c.head_dim != 256)
-            throw std::runtime_error("hip: head_dim must be 64, 128 or 256");
+        if (c.head_dim <= 0 || c.head_dim > 1024 || c.head_dim % 4 != 0)
+            throw std::runtime_error("hip: head_dim must be a multiple of 4 up to 1024");
         if (c.n_head % c.n_head_kv != 0) throw std::runtime_error("hip: n_head must be a multiple of n_head_kv");
         if (int(c.rope_inv_freq.size()) != c.head_dim / 2)
             throw std::runtime_error("hip: rope_inv_freq must have head_dim/2 entries");

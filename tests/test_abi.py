@@ -101,11 +101,14 @@ def test_host_validation(lib):
     ok = ia.decode_desc(24, 8, 128, 4096)
     assert lib.ingot_attn_decode_workspace_size(ctypes.byref(ok)) > 0
     assert ia.decode_splits(ok) >= 1
-    # decode covers head_dim 64 / 128 / 256 and any group size
+    # decode covers every head_dim up to 1024 (64 / 128 / 256 on the MFMA kernels, the others on
+    # the fallback kernel, which never splits) and any group size
     for good in (ia.decode_desc(32, 8, 64, 4096), ia.decode_desc(16, 8, 256, 4096),
-                 ia.decode_desc(40, 8, 128, 4096), ia.decode_desc(32, 1, 128, 100)):
+                 ia.decode_desc(40, 8, 128, 4096), ia.decode_desc(32, 1, 128, 100),
+                 ia.decode_desc(24, 8, 96, 4096), ia.decode_desc(4, 2, 1024, 9)):
         assert lib.ingot_attn_decode_workspace_size(ctypes.byref(good)) > 0
-    for bad in (ia.decode_desc(24, 8, 96, 4096),   # head_dim without a kernel
+    assert ia.decode_splits(ia.decode_desc(24, 8, 96, 4096)) == 1
+    for bad in (ia.decode_desc(24, 8, 1025, 4096), # head_dim above 1024
                 ia.decode_desc(24, 7, 128, 4096),  # not divisible
                 ia.decode_desc(512, 8, 128, 4096), # more query heads than epoch words
                 ia.decode_desc(24, 8, 128, 0)):    # no keys
@@ -114,7 +117,7 @@ def test_host_validation(lib):
     rc = lib.ingot_attn_decode(None, None, None, None, None, 0, ctypes.byref(ok), None)
     assert rc == -1
     rc = lib.ingot_attn_decode(None, None, None, None, None, 0,
-                               ctypes.byref(ia.decode_desc(24, 8, 96, 10)), None)
+                               ctypes.byref(ia.decode_desc(24, 8, 2048, 10)), None)
     assert rc == -2
     # one split needs no records; more splits need a record per (split, head)
     one = ia.decode_desc(24, 8, 128, 100)

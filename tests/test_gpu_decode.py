@@ -173,6 +173,21 @@ def test_decode_epochs_across_many_calls(dev, oracle_mod):
         assert_parity(got, want, f"call {i} L={L} splits={splits}")
 
 
+@pytest.mark.parametrize("n_head,n_head_kv,hd", [(32, 8, 80), (24, 8, 96), (12, 4, 112), (8, 2, 160),
+                                                  (4, 4, 20), (2, 1, 1024), (6, 3, 3)])
+@pytest.mark.parametrize("L", [1, 300, 2049])
+def test_decode_fallback_head_dims(dev, oracle_mod, n_head, n_head_kv, hd, L):
+    # Head sizes without an MFMA kernel run the fallback kernel, the counterpart of the
+    # reference's naive attention (shaders/kernels.metal:639-702, src/metal_backend.mm:373-382).
+    q, kb, vb = _inputs(60 + L + hd, n_head, n_head_kv, L, n_ctx=L + 3, hd=hd)
+    got = _run_decode(dev, q, kb, vb, n_head, n_head_kv, L, hd=hd)
+    want = oracle_mod.attn_decode(q, kb, vb, n_head, n_head_kv, hd, L, threads=8)
+    assert_parity(got, want, f"fallback hd={hd} G={n_head // n_head_kv} L={L}")
+    if L == 1:  # one key: the output is that key's V row, per KV head
+        v0 = vb[0].view(np.float16).astype(np.float32).reshape(n_head_kv, hd)
+        np.testing.assert_allclose(got.reshape(n_head, hd), np.repeat(v0, n_head // n_head_kv, axis=0), atol=1e-6)
+
+
 def _counters_all_zero(ws):
     import torch
 

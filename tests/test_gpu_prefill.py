@@ -220,3 +220,26 @@ def test_prefill_mfma_head_dims(dev, oracle_mod, hd, n_head, n_head_kv, pos, n_t
     got = _run_prefill(dev, q, kb, vb, n_head, n_head_kv, pos, n_tok, head_dim=hd)
     want = oracle_mod.attn_prefill(q, kb, vb, n_head, n_head_kv, hd, pos, n_tok, threads=16)
     assert_parity(got, want, f"prefill hd={hd} {n_head}/{n_head_kv} {n_tok}@{pos}")
+
+
+@pytest.mark.parametrize("hd,n_head,n_head_kv,pos,n_tok", [
+    (80, 32, 8, 0, 70), (96, 24, 8, 1000, 37), (112, 12, 4, 300, 5), (160, 8, 2, 0, 300),
+    (20, 4, 4, 17, 9), (1024, 2, 1, 260, 3), (3, 6, 3, 0, 40)])
+def test_prefill_fallback_head_dims(dev, oracle_mod, hd, n_head, n_head_kv, pos, n_tok):
+    # Head sizes without an MFMA kernel run the fallback kernel, the counterpart of the
+    # reference's naive attention (shaders/kernels.metal:639-702, chosen at
+    # src/metal_backend.mm:373-382 for every head_dim but 128).
+    import ingot_attn as ia
+
+    d = ia.prefill_desc(n_head, n_head_kv, hd, pos, n_tok)
+    assert ia.prefill_splits(d) == 1
+    rng = np.random.Generator(np.random.PCG64(11 * n_head + pos + hd))
+    L = pos + n_tok
+    q = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
+    kb = np.full((L + 5, n_head_kv * hd), 0x7E00, dtype=np.uint16)  # NaN past the chunk
+    vb = np.full((L + 5, n_head_kv * hd), 0x7E00, dtype=np.uint16)
+    kb[:L] = rng.standard_normal((L, n_head_kv * hd)).astype(np.float16).view(np.uint16)
+    vb[:L] = rng.standard_normal((L, n_head_kv * hd)).astype(np.float16).view(np.uint16)
+    got = _run_prefill(dev, q, kb, vb, n_head, n_head_kv, pos, n_tok, head_dim=hd)
+    want = oracle_mod.attn_prefill(q, kb, vb, n_head, n_head_kv, hd, pos, n_tok, threads=8)
+    assert_parity(got, want, f"fallback prefill hd={hd} {n_head}/{n_head_kv} {n_tok}@{pos}")
