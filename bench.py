@@ -285,10 +285,12 @@ def cpu_baseline(W, seconds):
 # each: (name, n_head, n_head_kv, head_dim, n_keys) for decode, (..., pos, n_tok) for prefill.
 ENVELOPE_DECODE = (("decode-64/8-hd128-4096", 64, 8, 128, 4096),
                    ("decode-32/8-hd64-4096", 32, 8, 64, 4096),
-                   ("decode-16/8-hd256-4096", 16, 8, 256, 4096))
+                   ("decode-16/8-hd256-4096", 16, 8, 256, 4096),
+                   ("decode-24/8-hd96-4096", 24, 8, 96, 4096))  # the fallback kernel (attn_naive.hip)
 ENVELOPE_PREFILL = (("prefill-32/8-hd128-512@3584", 32, 8, 128, 3584, 512),
                     ("prefill-32/8-hd64-512@3584", 32, 8, 64, 3584, 512),
-                    ("prefill-16/8-hd256-512@3584", 16, 8, 256, 3584, 512))
+                    ("prefill-16/8-hd256-512@3584", 16, 8, 256, 3584, 512),
+                    ("prefill-24/8-hd96-128@0", 24, 8, 96, 0, 128))  # the fallback kernel
 
 
 def envelope(torch, ia, steps, warmup, use_graph):

@@ -198,9 +198,10 @@ int ingot_proj_rope_kv(const void* const* w, const float* x, const float* norm_w
          : lrc == -1 ? INGOT_ATTN_EINVAL : INGOT_ATTN_EHIP;
 }
 
-// Decode split count (1 for the fallback kernel, which never splits).
+// Decode split count (the fallback kernel chooses its own key slices).
 uint32_t decode_split_count(const IngotAttnDecodeDesc* d) {
-    return mfma_head_dim(d->head_dim) ? ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits) : 1u;
+    return mfma_head_dim(d->head_dim) ? ingot::decode_splits(d->n_keys, d->head_dim, d->n_splits)
+                                      : ingot::attn_any_slices(d->n_keys, 1);
 }
 
 uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d) {
@@ -224,6 +225,8 @@ uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d) {
 size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d) {
     if (check_decode(d)) return 0;
     const uint32_t splits = decode_split_count(d);
+    if (!mfma_head_dim(d->head_dim))  // the fallback kernel's slice records
+        return kCounterBytes + (splits > 1 ? size_t(d->n_head) * splits * (d->head_dim + 2) * sizeof(float) : 0);
     return kCounterBytes + (splits > 1 ? size_t(d->n_head) * ingot::kDecodeHeadRecordBytes : 0);
 }
 
@@ -251,8 +254,9 @@ int ingot_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
     const auto* k = reinterpret_cast<const _Float16*>(k_cache) + d->kv_offset;
     const auto* v = reinterpret_cast<const _Float16*>(v_cache) + d->kv_offset;
     const int lrc = !mfma_head_dim(d->head_dim)
-        ? ingot::launch_attn_any(q, k, v, out, d->n_keys - 1, 1, d->n_head * d->head_dim, d->n_head, d->n_head_kv,
-                                 d->head_dim, d->scale, static_cast<hipStream_t>(stream))
+        ? ingot::launch_attn_any(q, k, v, out, reinterpret_cast<float*>(static_cast<char*>(workspace) + kCounterBytes),
+                                 d->n_keys - 1, 1, d->n_head * d->head_dim, d->n_head, d->n_head_kv, d->head_dim,
+                                 d->scale, static_cast<hipStream_t>(stream))
         : ingot::launch_decode(q, k, v, out, workspace, d->n_keys, splits, d->n_head_kv,
                                          d->n_head / d->n_head_kv, d->head_dim, d->scale,
                                          static_cast<hipStream_t>(stream));
@@ -276,8 +280,8 @@ int ingot_attn_prefill(const float* q, const uint16_t* k_cache, const uint16_t* 
     const uint32_t splits = prefill_split_count(d);
     char* part = static_cast<char*>(workspace) + prefill_part_offset(d->n_head);
     const int lrc = !mfma_head_dim(d->head_dim)
-        ? ingot::launch_attn_any(q, k, v, out, d->pos, d->n_tok, d->q_stride, d->n_head, d->n_head_kv, d->head_dim,
-                                 d->scale, st)
+        ? ingot::launch_attn_any(q, k, v, out, nullptr, d->pos, d->n_tok, d->q_stride, d->n_head, d->n_head_kv,
+                                 d->head_dim, d->scale, st)
         : ingot::launch_prefill(q, k, v, out, part, d->pos, d->n_tok, d->q_stride, d->n_head_kv,
                                           d->n_head / d->n_head_kv, d->head_dim, splits, d->scale, st);
     return lrc == 0 ? INGOT_ATTN_OK : lrc == -2 ? INGOT_ATTN_EUNSUPPORTED

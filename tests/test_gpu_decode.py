@@ -175,7 +175,7 @@ def test_decode_epochs_across_many_calls(dev, oracle_mod):
 
 @pytest.mark.parametrize("n_head,n_head_kv,hd", [(32, 8, 80), (24, 8, 96), (12, 4, 112), (8, 2, 160),
                                                   (4, 4, 20), (2, 1, 1024), (6, 3, 3)])
-@pytest.mark.parametrize("L", [1, 300, 2049])
+@pytest.mark.parametrize("L", [1, 300, 2049, 5000])
 def test_decode_fallback_head_dims(dev, oracle_mod, n_head, n_head_kv, hd, L):
     # Head sizes without an MFMA kernel run the fallback kernel, the counterpart of the
     # reference's naive attention (shaders/kernels.metal:639-702, src/metal_backend.mm:373-382).
