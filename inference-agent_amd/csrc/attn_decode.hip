@@ -242,8 +242,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     }
     const size_t head = size_t(kvh) * G + h;
     if (n_splits == 1) {
-        if (lane < 32)
-            *reinterpret_cast<float4v*>(out + head * kHeadDim + 4 * j) = O * (L > 0.f ? 1.f / L : 0.f);
+        if (lane < 32) handoff::store_out(out + head * kHeadDim, kHeadDim * 4, 16 * j, O * (L > 0.f ? 1.f / L : 0.f));
         return;
     }
 

@@ -260,7 +260,7 @@ __global__ __launch_bounds__(64 * kNW) void attn_decode_kernel(
         const uint32_t head = head0 + h;
         float* dst = out + size_t(head) * HD;
         if (!multi) {
-            if (lane < OL) *reinterpret_cast<float4v*>(dst + d0) = O * (L > 0.f ? 1.f / L : 0.f);
+            if (lane < OL) handoff::store_out(dst, HD * 4, 4 * d0, O * (L > 0.f ? 1.f / L : 0.f));
             continue;
         }
         // The split hand-off (decode_merge.h): store this head's record, count it in, and the

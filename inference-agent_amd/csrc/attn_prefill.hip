@@ -46,6 +46,7 @@ namespace {
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __fp16 fp16x4 __attribute__((__vector_size__(8)));  // operand type of ds_read_tr16_b64
 typedef __attribute__((address_space(3))) fp16x4 lds_fp16x4;
 typedef __attribute__((address_space(3))) half8 lds_half8;
@@ -54,6 +55,7 @@ typedef __attribute__((address_space(3))) half8 lds_half8;
 template <int HD> constexpr int kBN = HD == 256 ? 32 : 64;
 constexpr float kLazy = 8.f;                   // base-2 headroom before the reference max moves
 constexpr int kBufferFlags = 0x00020000;       // buffer descriptor word 3 (raw, 32-bit format)
+constexpr int kScDevice = 16;                  // buffer cache-policy bits: sc1 = device scope
 // LDS geometry for head size HD: a K/V row of HD halves (no padding), 16-byte chunks per row,
 // a K or V tile of kBN rows, a stage = K tile + V tile (HD 128: 256 B, 16, 16 KB, 32 KB).
 template <int HD> constexpr int kRowBytes = HD * 2;
@@ -516,13 +518,21 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
     const bool live = row < n_tok;
     if (n_splits == 1) {  // the whole key range: write the output
         if (!owner || !live) return;
+        // Write-through (sc1) stores: the output leaves no dirty lines in the L2 for the
+        // end-of-dispatch write-back (measured: C2 11.75 -> 11.19 us, C4 39.8 -> 38.5; a
+        // nontemporal store gained less).
+        const __amdgpu_buffer_rsrc_t ors = __builtin_amdgcn_make_buffer_rsrc(
+            out + size_t(qblk0) * q_stride, 0, int(min(uint64_t(64) * q_stride * 4, uint64_t(0x7fffffff))),
+            kBufferFlags);
 #pragma unroll
         for (int h = 0; h < G; h++) {
             const uint32_t head = kvh * G + h;
             const float inv = l[h] > 0.f ? 1.f / l[h] : 0.f;
-            float* dst = out + size_t(row) * q_stride + size_t(head) * HD + 4 * g;
+            const int off = int(4 * ((row - qblk0) * q_stride + head * HD + 4 * g));
 #pragma unroll
-            for (int d = 0; d < ND; d++) *reinterpret_cast<float4v*>(dst + 16 * d) = O[h][d] * inv;
+            for (int d = 0; d < ND; d++)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, O[h][d] * inv), ors, off + 64 * d, 0,
+                                                       kScDevice);
         }
         return;
     }
@@ -541,10 +551,16 @@ void attn_prefill_kernel(const float* __restrict__ q, const _Float16* __restrict
 #pragma unroll
         for (int d = 0; d < ND; d++) {
             const float4v v = O[h][d] * inv;
-            *reinterpret_cast<half4*>(dst + 2 * (16 * d + 4 * g)) =
-                half4{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])};
+            // device-scope (write-through) 8-byte stores, like the output (C4 39.6 -> 38.7 us)
+            __hip_atomic_store(reinterpret_cast<unsigned long long*>(dst + 2 * (16 * d + 4 * g)),
+                               __builtin_bit_cast(unsigned long long,
+                                                  half4{_Float16(v[0]), _Float16(v[1]), _Float16(v[2]), _Float16(v[3])}),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        if (g == 0) *reinterpret_cast<float4v*>(dst + 2 * HD) = float4v{started[h] ? m[h] : kNoMax, l[h], 0.f, 0.f};
+        if (g == 0)
+            __hip_atomic_store(reinterpret_cast<unsigned long long*>(dst + 2 * HD),
+                               __builtin_bit_cast(unsigned long long, float2{started[h] ? m[h] : kNoMax, l[h]}),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -595,7 +611,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_prefill_combine(
         }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    *reinterpret_cast<float4v*>(out + size_t(row) * q_stride + size_t(h) * HD + d) = O * inv;
+    __builtin_nontemporal_store(O * inv, reinterpret_cast<float4v*>(out + size_t(row) * q_stride + size_t(h) * HD + d));
 }
 
 constexpr int kQW = 4;  // query waves per workgroup (16 queries x G heads each)

@@ -75,6 +75,15 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t head_region(char* recs, uint32
                                              uint32_t(kDecodeHeadRecordBytes), kBufferFlags);
 }
 
+// 16 bytes of output at byte offset `off` of `row` with a write-through (sc1) store: the output
+// then leaves no dirty line in the L2 for the end-of-dispatch write-back (measured: C3 decode
+// 8.04 -> 7.92 us, 8192 keys 10.60 -> 10.46; a nontemporal store gained nothing).
+// `bytes` (wave-uniform) is the row's size: the buffer descriptor covers the row.
+__device__ __forceinline__ void store_out(float* row, int bytes, int off, float4v v) {
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(row, 0, bytes, kBufferFlags);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rs, off, 0, kScDevice);
+}
+
 // Steps 1 and 2 for one head, called by a whole wave: lane l holds dims 4c..4c+3 of o,
 // c = l % (HD/4) (lanes with the same c hold the same values); (m, l) are wave-uniform. Returns
 // the counter's old value (wave-uniform).
@@ -146,7 +155,7 @@ __device__ __forceinline__ void merge_records(__amdgpu_buffer_rsrc_t rs, unsigne
         acc[e] = a;
     }
     __builtin_amdgcn_wave_barrier();
-    if (sg == 0) *reinterpret_cast<float4v*>(out + 4 * c) = acc * (Lt > 0.f ? 1.f / Lt : 0.f);
+    if (sg == 0) store_out(out, HD * 4, 16 * c, acc * (Lt > 0.f ? 1.f / Lt : 0.f));
     if (lane == 0)  // leave the workspace ready for the next call
         __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
