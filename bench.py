@@ -40,7 +40,7 @@ sys.path.insert(0, os.path.join(ROOT, "inference-agent_amd"))
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
 # HBM bytes per C3 decode launch: (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) KiB from rocprofv3, the
 # factors from the copy probe (profiles/attn_decode_C3_traffic.md).
-C3_TRAFFIC_BYTES = int((8466.0 * 2.0 + 456.75) * 1024)
+C3_TRAFFIC_BYTES = int((8465.0 * 2.0 + 444.75) * 1024)
 C3_TRAFFIC_SOURCE = ("profiles/attn_decode_C3_traffic.md: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 "
                      "of attn_decode_kernel<3,4,false> (inference-agent_amd/csrc/attn_decode.hip)")
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 MFMA, 2.5 PFLOP/s
