@@ -8,6 +8,11 @@
 //   probe_mfma: back-to-back f16 MFMAs with no memory traffic (independent accumulator chains
 //               per wave: 8 of 32x32x16 or 16 of 16x16x32), the achievable matrix-core rate that the
 //               prefill kernels are measured against next to the 2.5 PFLOP/s spec figure.
+//   probe_count / probe_handoff: the memory-order facts the decode kernels' split hand-off rests
+//               on (decode_merge.h), checked across XCDs: a relaxed device-scope atomic counts
+//               exactly whichever XCD each workgroup runs on, and a device-scope store, a wait
+//               for its acknowledgement and a counter increment make the store visible to the
+//               device-scope loads of the workgroup that counts last, wherever that one runs.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -83,5 +88,54 @@ extern "C" int ingot_probe_copy(const void* src, void* dst, size_t bytes, uint32
                                 void* stream) {
     hipLaunchKernelGGL(probe_copy, dim3(n_blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                        static_cast<const float4v*>(src), static_cast<float4v*>(dst), bytes / 16);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// Hardware id of the XCD (accelerator complex die) the wave runs on (gfx940+ HW_REG_XCC_ID).
+__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg((3 << 11) | 20) & 15; }
+
+__global__ __launch_bounds__(64) void probe_count(unsigned* __restrict__ ctr, unsigned* __restrict__ ret,
+                                                  unsigned* __restrict__ xcc) {
+    if (threadIdx.x != 0) return;
+    ret[blockIdx.x] = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    xcc[blockIdx.x] = xcc_id();
+}
+
+typedef unsigned u32x4p __attribute__((ext_vector_type(4)));
+constexpr int kProbeBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw, 32-bit format)
+constexpr int kProbeScDevice = 16;             // cache-policy bits: sc1 = device scope
+
+// Workgroup b stores b + 1 into slot b (device scope), waits for the acknowledgement, counts
+// itself in; the last one reads every slot with device-scope loads: res = {sum, slots that did
+// not hold their value, the last one's XCD}.
+__global__ __launch_bounds__(64) void probe_handoff(unsigned* __restrict__ ctr, unsigned* __restrict__ slot,
+                                                    unsigned* __restrict__ res, unsigned n) {
+    if (threadIdx.x != 0) return;
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(slot, 0, int(n * 4), kProbeBufferFlags);
+    __builtin_amdgcn_raw_buffer_store_b32(blockIdx.x + 1, rs, int(blockIdx.x * 4), 0, kProbeScDevice);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    const unsigned p = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (p != n - 1) return;
+    unsigned sum = 0, bad = 0;
+    for (unsigned i = 0; i < n; i++) {
+        const unsigned v = __builtin_amdgcn_raw_buffer_load_b32(rs, int(i * 4), 0, kProbeScDevice);
+        sum += v;
+        bad += v != i + 1;
+    }
+    res[0] = sum;
+    res[1] = bad;
+    res[2] = xcc_id();
+}
+
+extern "C" int ingot_probe_count(unsigned* ctr, unsigned* ret, unsigned* xcc, uint32_t n_blocks, void* stream) {
+    hipLaunchKernelGGL(probe_count, dim3(n_blocks), dim3(64), 0, static_cast<hipStream_t>(stream), ctr, ret, xcc);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+extern "C" int ingot_probe_handoff(unsigned* ctr, unsigned* slot, unsigned* res, uint32_t n_blocks, void* stream) {
+    hipLaunchKernelGGL(probe_handoff, dim3(n_blocks), dim3(64), 0, static_cast<hipStream_t>(stream), ctr, slot, res,
+                       n_blocks);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
