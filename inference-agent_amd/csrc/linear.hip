@@ -32,6 +32,7 @@ namespace {
 
 typedef float float16v_ __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 (raw, 32-bit format)
 
@@ -972,6 +973,15 @@ __device__ __forceinline__ void load_raw_lds(Raw<T>& r, const uint8_t* row, uint
         const uint8_t* b = row + 34 * (k0 / 32);
         r.d = ld_u16(b);
         for (int s = 0; s < 2; s++) lds_8bytes(b + 2 + 16 * s + 8 * h, r.q[s][0], r.q[s][1]);
+    } else if constexpr (T == kQ6_K) {  // `row` is the block (a stage holds one)
+        const uint32_t e = k0 % 256, hh = e / 128, g = (e % 128) / 32;
+        r.d = ld_u16(row + 208);
+        r.sc = ld_u16(row + 192 + hh * 8 + 2 * g);
+        for (int s = 0; s < 2; s++) {
+            const uint32_t l = 16 * s + 8 * h;
+            lds_8bytes(row + hh * 64 + 32 * (g & 1) + l, r.ql[s][0], r.ql[s][1]);
+            lds_8bytes(row + 128 + hh * 32 + l, r.qh[s][0], r.qh[s][1]);
+        }
     } else {
         load_raw<T>(r, row, k0, h);
     }
@@ -1040,13 +1050,16 @@ __device__ __forceinline__ half8 frag(const Raw<T>& r, int s, uint32_t k0) {
         const int sh = 4 * s;  // elements 16..31 of the block are the high nibbles
         for (int i = 0; i < 8; i++) o[i] = _Float16(d * float((byte_of(r.q[0], r.q[1], i) >> sh) & 0xF) + m);
     } else if constexpr (T == kQ6_K) {
+        // Four 6-bit values per word (low nibbles from ql, two high bits from qh, byte-wise),
+        // each converted from its byte; sc*(q - 32) is formed as fma(sc, q, -32*sc): -32*sc is
+        // exact and the fma rounds the exact sc*q - 32*sc once, the same f32 value.
         const uint32_t g = (k0 % 128) / 32;
         const float sc = f16_bits(r.d) * float(int8_t((r.sc >> (8 * s)) & 0xFF));
-        const int shl = g >= 2 ? 4 : 0, shh = 2 * int(g);
-        for (int i = 0; i < 8; i++) {
-            const int q = int(((byte_of(r.ql[s][0], r.ql[s][1], i) >> shl) & 0xF) |
-                              (((byte_of(r.qh[s][0], r.qh[s][1], i) >> shh) & 3) << 4));
-            o[i] = _Float16(sc * float(q - 32));
+        const float c = -32.f * sc;
+        const uint32_t shl = g >= 2 ? 4 : 0, shh = 2 * g;
+        for (int w = 0; w < 2; w++) {
+            const uint32_t q = ((r.ql[s][w] >> shl) & 0x0F0F0F0Fu) | (((r.qh[s][w] >> shh) & 0x03030303u) << 4);
+            for (int b = 0; b < 4; b++) o[4 * w + b] = _Float16(__builtin_fmaf(sc, float((q >> (8 * b)) & 0xFF), c));
         }
     }
     return o;
@@ -1063,15 +1076,20 @@ constexpr int kOutStage = 32 * kOutPitch;
 
 // W staged through LDS (LW kernels): a stage is `ks` elements of every row of the tile, `bytes`
 // per row (a whole number of 16-byte chunks, so lanes load full cache lines), stored at a row
-// pitch that keeps the B-operand reads free of bank conflicts. Q6_K has no entry (its 210-byte
-// blocks do not tile rows into 16-byte pieces of a size that fits): it uses the direct path.
-template <int T> struct Stage { static constexpr uint32_t ks = 0, bytes = 0, pitch = 0; static constexpr bool swz = false; };
-template <> struct Stage<kF32>  { static constexpr uint32_t ks = 32,  bytes = 128, pitch = 128; static constexpr bool swz = true; };
-template <> struct Stage<kF16>  { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 128; static constexpr bool swz = true; };
-template <> struct Stage<kBF16> { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 128; static constexpr bool swz = true; };
-template <> struct Stage<kQ8_0> { static constexpr uint32_t ks = 256, bytes = 272, pitch = 272; static constexpr bool swz = false; };
-template <> struct Stage<kQ4_0> { static constexpr uint32_t ks = 256, bytes = 144, pitch = 144; static constexpr bool swz = false; };
-template <> struct Stage<kQ4_1> { static constexpr uint32_t ks = 256, bytes = 160, pitch = 176; static constexpr bool swz = false; };
+// pitch that keeps the B-operand reads free of bank conflicts.
+// `win`: the stage's bytes do not start on a 16-byte boundary (Q6_K: 210-byte blocks, rows of
+// 210 * n_in / 256 bytes), so each row's stage is loaded as the 16-byte aligned window that holds
+// it (14 chunks hold the 210 bytes at any even shift) and read at the row's shift within it. The
+// pitch of 232 bytes (58 dwords: 32 rows on distinct banks) is 8-byte aligned, so a window chunk
+// goes to LDS as two 8-byte writes.
+template <int T> struct Stage { static constexpr uint32_t ks = 0, bytes = 0, pitch = 0; static constexpr bool swz = false, win = false; };
+template <> struct Stage<kF32>  { static constexpr uint32_t ks = 32,  bytes = 128, pitch = 128; static constexpr bool swz = true, win = false; };
+template <> struct Stage<kF16>  { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 128; static constexpr bool swz = true, win = false; };
+template <> struct Stage<kBF16> { static constexpr uint32_t ks = 64,  bytes = 128, pitch = 128; static constexpr bool swz = true, win = false; };
+template <> struct Stage<kQ8_0> { static constexpr uint32_t ks = 256, bytes = 272, pitch = 272; static constexpr bool swz = false, win = false; };
+template <> struct Stage<kQ4_0> { static constexpr uint32_t ks = 256, bytes = 144, pitch = 144; static constexpr bool swz = false, win = false; };
+template <> struct Stage<kQ4_1> { static constexpr uint32_t ks = 256, bytes = 160, pitch = 176; static constexpr bool swz = false, win = false; };
+template <> struct Stage<kQ6_K> { static constexpr uint32_t ks = 256, bytes = 224, pitch = 232; static constexpr bool swz = false, win = true; };
 
 // 16-byte chunk swizzles of the LDS stages (XOR of the chunk index with a function of the row)
 // so that the 16-row b128 reads and the 2-row (b128) or 4-row (b64) write groups each touch 64
@@ -1176,7 +1194,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         constexpr uint32_t NCH = (RT * CH + 511) / 512;      // chunks per thread per matrix
         // x stages of XK elements (NXS per W stage), as large as the LDS left by the W double
         // buffer allows
-        constexpr uint32_t XK = T == kQ8_0 || (TT == 2 && T == kQ4_0) ? 64 : (KS < 128 ? KS : 128);
+        constexpr uint32_t XK = T == kQ8_0 || (TT == 2 && (T == kQ4_0 || T == kQ6_K)) ? 64 : (KS < 128 ? KS : 128);
         constexpr uint32_t NXS = KS / XK, PX = XK / kMmK;  // x stages per W stage, steps per x stage
         constexpr uint32_t XP = XK;        // halves per token row of an x stage (chunks swizzled)
         constexpr uint32_t XF4 = XK / 32;  // float4 x loads per thread per x stage
@@ -1190,18 +1208,37 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         // One descriptor per staged matrix (a load instruction never mixes them: a per-lane
         // choice would make the compiler loop over the wave's distinct descriptors).
         const uint32_t rows_here = min(n_out - rtl * RT, RT);
+        // WIN: each descriptor starts at the 16-byte boundary at or below its tile's first row,
+        // a0[m] bytes before it, and ends at the 16-byte boundary at or above its last byte: a
+        // 16-byte load that crosses the end of the range returns zeros as a whole, and the
+        // chunk that holds the tile's last byte lies in that byte's page.
+        constexpr bool WIN = Stage<T>::win;
         __amdgpu_buffer_rsrc_t wrs[NM];
-        for (uint32_t m = 0; m < NM; m++)
-            wrs[m] = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint8_t*>((PAIR ? (m == 0 ? mats.W[0] : mats.W[1]) : W) + size_t(rtl) * RT * row_bytes),
-                0, int(rows_here * row_bytes), kBufferFlags);
+        uint32_t a0[NM];
+        for (uint32_t m = 0; m < NM; m++) {
+            const uint8_t* wb = (PAIR ? (m == 0 ? mats.W[0] : mats.W[1]) : W) + size_t(rtl) * RT * row_bytes;
+            a0[m] = WIN ? uint32_t(reinterpret_cast<uintptr_t>(wb)) & 15u : 0u;
+            const uint32_t span = rows_here * row_bytes + a0[m];
+            wrs[m] = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wb - a0[m]), 0,
+                                                       int(WIN ? (span + 15) & ~15u : span), kBufferFlags);
+        }
         const uint32_t kbyte0 = kbeg / Fmt<T>::blk * Fmt<T>::bytes;
-        uint32_t goff[NCH], loff[NCH];
+        // goff: the chunk's byte offset in the tile (WIN: of its row's stage 0, the chunk's own
+        // 16 * o in o16; the window start is aligned per stage)
+        uint32_t goff[NCH], loff[NCH], o16[NCH];
         for (uint32_t i = 0; i < NCH; i++) {
             const uint32_t c = min(tid + 512 * i, RT * CH - 1);
             const uint32_t r = c / CH, o = c % CH;
-            goff[i] = min(r, rows_here - 1) * row_bytes + kbyte0 + 16 * o;
+            goff[i] = min(r, rows_here - 1) * row_bytes + kbyte0 + (WIN ? 0u : 16 * o);
+            o16[i] = 16 * o;
             loff[i] = r * PITCH + 16 * (Stage<T>::swz ? o ^ swz128(r) : o);  // matrix m's rows follow at m * RT * PITCH
+        }
+        // WIN: the shift of the wave's rows (row block jb, lane row n) within their windows at
+        // stage 0; a block is 210 = 13 * 16 + 2 bytes, so stage j adds 2j (mod 16).
+        uint32_t wsh0[NB];
+        for (uint32_t jb = 0; jb < NB; jb++) {
+            const uint32_t tr = min(lrow0 - (PAIR ? mat * RT : 0u) + 32 * jb + n, rows_here - 1);
+            wsh0[jb] = WIN ? (a0[PAIR ? mat : 0] + tr * row_bytes + kbyte0) & 15u : 0u;
         }
         u32x4 wr[2][NM][NCH];
         // The tile's 128-token group g walks its stages starting at stage g * nst / groups and
@@ -1213,18 +1250,28 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         const uint32_t rot = uint32_t(__builtin_amdgcn_readfirstlane(int(tok0 / 128 * nst / groups % nst)));
         auto phys = [&](uint32_t j) { j = min(j, nst - 1) + rot; return j >= nst ? j - nst : j; };
         auto load_w = [&](int slot, uint32_t j) {
-            const uint32_t sb = phys(j) * SB;
+            const uint32_t sb = phys(j) * (WIN ? Fmt<T>::bytes : SB);
             for (uint32_t m = 0; m < NM; m++)
-                for (uint32_t i = 0; i < NCH; i++)
+                for (uint32_t i = 0; i < NCH; i++) {
+                    const uint32_t off = WIN ? ((a0[m] + goff[i] + sb) & ~15u) + o16[i] : goff[i] + sb;
                     wr[slot][m][i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                   wrs[m], int(goff[i] + sb), 0, 0));
+                                                                   wrs[m], int(off), 0, 0));
+                }
         };
         auto store_w = [&](int slot) {
             uint8_t* base = wsm + slot * (kMmRows * PITCH);
             for (uint32_t m = 0; m < NM; m++)
                 for (uint32_t i = 0; i < NCH; i++)
-                    if (tid + 512 * i < RT * CH)
-                        *reinterpret_cast<u32x4*>(base + m * RT * PITCH + loff[i]) = wr[slot][m][i];
+                    if (tid + 512 * i < RT * CH) {
+                        uint8_t* dst = base + m * RT * PITCH + loff[i];
+                        if constexpr (WIN) {
+                            const u32x4 v = wr[slot][m][i];
+                            *reinterpret_cast<u32x2*>(dst) = u32x2{v[0], v[1]};
+                            *reinterpret_cast<u32x2*>(dst + 8) = u32x2{v[2], v[3]};
+                        } else {
+                            *reinterpret_cast<u32x4*>(dst) = wr[slot][m][i];
+                        }
+                    }
         };
         const uint32_t xk = 4 * (tid % 8);
         uint32_t xso[TT];
@@ -1271,6 +1318,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                 const uint32_t j = j0 + jj;
                 if (j >= nst) break;
                 const uint8_t* wrow = wsm + jj * (kMmRows * PITCH) + (lrow0 + n) * PITCH;
+                const uint32_t wsh_j = WIN ? 2 * phys(j) : 0u;  // (before load_w's phys(j + 2))
                 load_w(jj, j + 2);  // this slot's stage j is already in LDS
                 // Issue the prefetch here: left to the scheduler, these loads sink below the
                 // stage's MFMAs and the next stage waits for them.
@@ -1286,7 +1334,7 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
                         half8 b[NB][2];
 #pragma unroll
                         for (uint32_t jb = 0; jb < NB; jb++) {
-                            const uint8_t* wr_j = wrow + 32 * jb * PITCH;
+                            const uint8_t* wr_j = wrow + 32 * jb * PITCH + (WIN ? (wsh0[jb] + wsh_j) & 15u : 0u);
                             Raw<T> r;
                             if constexpr (Stage<T>::swz) {
                                 const uint32_t sw = swz128(lrow0 + 32 * jb + n);
@@ -1397,7 +1445,12 @@ __global__ __launch_bounds__(512) void linear_matmul_kernel(
         // arrival is counted, and the last split reads the partials with device-scope loads, which
         // do not take a clean L2 line: the hand-off needs no release/acquire pair, whose L2
         // writeback and invalidate around the atomic would cost more than the whole tail.
+        // Compiler-only fences on both sides of the wait keep the optimizer from moving the
+        // stores past it or the counter increment before it; the hardware order comes from the
+        // wait and the barrier.
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(0);  // the partial has reached device scope
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __syncthreads();
         __shared__ unsigned int last;
         if (tid == 0) {
@@ -1526,7 +1579,7 @@ int launch_mm_t(MmMats mats, uint32_t n_mats, const float* x, uint32_t n_in, uin
     }
     // LDS-staged W when rows split into whole 16-byte stage pieces.
     constexpr uint32_t KS = Stage<T>::ks;
-    const bool lw = KS != 0 && row_bytes % 16 == 0 && n_in % (KS != 0 ? KS : 1) == 0;
+    const bool lw = KS != 0 && (Stage<T>::win || row_bytes % 16 == 0) && n_in % (KS != 0 ? KS : 1) == 0;
     // Tiles of 128 tokens (two halves; waves of 64 x 64: each A operand read from LDS feeds two
     // MFMAs and each W stage serves twice the tokens) for unsplit calls when they take fewer
     // rounds of 256 workgroups: a 128-token tile costs ~1.8x a 64-token one (Q4_0 gate/up at

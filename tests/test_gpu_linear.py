@@ -178,14 +178,16 @@ def test_split_k_is_deterministic(dev, oracle_mod, n_tok):
     _close(a, oracle_mod.linear(t, raw, x, n, n, f16_path=True), f"split n_tok={n_tok}")
 
 
+@pytest.mark.parametrize("t", ["Q8_0", "Q6_K"])
 @pytest.mark.parametrize("n_splits", [2, 3, 5, 8])
-def test_requested_splits(dev, oracle_mod, n_splits):
+def test_requested_splits(dev, oracle_mod, t, n_splits):
     """An explicit split count (uneven last split for 3 and 5 over 96 k steps) gives the same
-    result as no split, within f32 rounding, and matches the oracle."""
+    result as no split, within f32 rounding, and matches the oracle. (Q6_K: a split starts at a
+    210-byte block boundary, so each split's LDS windows sit at their own shifts.)"""
     import torch
     import ingot_attn as ia
 
-    t, n, n_tok = "Q8_0", 3072, 100
+    n, n_tok = 3072, 100
     raw = gb.random_weights(t, n, n, seed=41)
     x = _x(n_tok, n, seed=42)
     d = ia.linear_desc(t, n, n, n_tok, n_splits=n_splits)
@@ -199,12 +201,13 @@ def test_requested_splits(dev, oracle_mod, n_splits):
     _close(got, oracle_mod.linear(t, raw, x, n, n, f16_path=True), f"n_splits={n_splits}")
 
 
-@pytest.mark.parametrize("t", ["F16", "BF16", "F32", "Q4_0", "Q4_1"])
+@pytest.mark.parametrize("t", ["F16", "BF16", "F32", "Q4_0", "Q4_1", "Q6_K"])
 @pytest.mark.parametrize("n_out", [2000, 2001])
 def test_batched_128_token_tiles(dev, oracle_mod, t, n_out):
     """Enough token tiles for two rounds of 64-token tiles take one round of 128-token tiles
     (waves of 64 tokens x 64 rows); ragged n_tok and n_out (2001: rows not 16-byte aligned, the
-    scalar output path), with the residual add. Matches the f16-path oracle."""
+    scalar output path), with the residual add. Matches the f16-path oracle. (Q6_K rows of 210
+    bytes: the last tile's last block ends inside a 16-byte chunk.)"""
     n_in, n_tok = 256, 2100  # 8 x 33 tiles of 64 tokens, 8 x 17 of 128
     raw = gb.random_weights(t, n_out, n_in, seed=55)
     x = _x(n_tok, n_in, seed=56)
