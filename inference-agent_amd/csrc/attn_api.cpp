@@ -17,7 +17,10 @@ namespace {
 
 using ingot::kCounterBytes;
 
-size_t prefill_part_offset(uint32_t n_head) { return kCounterBytes + size_t(n_head) * ingot::kDecodeHeadRecordBytes; }
+// The prefill records start right after the counters, where decode calls keep their records:
+// every call writes the records it reads (after its own counters say they are there), so the two
+// kinds of call can share one workspace, ordered on one stream.
+size_t prefill_part_offset(uint32_t) { return kCounterBytes; }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -235,8 +238,6 @@ size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d) {
     const uint32_t splits = prefill_split_count(d);
     const size_t parts = splits > 1 ? size_t(splits) * d->n_tok * d->n_head *
                                           ingot::prefill_record_bytes(d->head_dim) : 0;
-    // The prefill records follow the decode record regions of the same heads, so a workspace
-    // shared by decode and prefill calls never holds prefill data where decode tags are read.
     return prefill_part_offset(d->n_head) + parts;
 }
 

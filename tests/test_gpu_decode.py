@@ -251,3 +251,44 @@ def test_decode_closed_forms(dev):
     got = _run_decode(dev, q, k.view(np.uint16), v.view(np.uint16), H, HKV, 300).reshape(H, HD)
     mean = v.astype(np.float64).reshape(300, HKV, HD).mean(axis=0)
     np.testing.assert_allclose(got, np.repeat(mean, 3, axis=0), atol=1e-5)
+
+
+def test_decode_and_prefill_share_one_workspace(dev):
+    # Decode and split prefill calls keep their records in the same part of one workspace
+    # (right after the counters); each call writes the records it reads, so interleaving them
+    # changes no bit of any result, and the counters are back at zero after every call.
+    import torch
+    import ingot_attn as ia
+
+    ws = ia.Workspace(dev)
+    ws.get(1 << 24)
+    L, pos, n_tok = 3000, 1000, 100
+    rng = np.random.Generator(np.random.PCG64(91))
+    kb = rng.standard_normal((L, KV)).astype(np.float16).view(np.uint16)
+    vb = rng.standard_normal((L, KV)).astype(np.float16).view(np.uint16)
+    kd, vd = _t(kb.view(np.int16), dev), _t(vb.view(np.int16), dev)
+    qdec = _t(rng.standard_normal(H * HD).astype(np.float32), dev)
+    qpre = _t(rng.standard_normal((n_tok, H * HD)).astype(np.float32), dev)
+    calls = [("decode", ia.decode_desc(H, HKV, HD, L)),
+             ("prefill", ia.prefill_desc(H, HKV, HD, pos, n_tok, n_splits=4)),
+             ("decode", ia.decode_desc(H, HKV, HD, 2000, n_splits=7)),
+             ("prefill", ia.prefill_desc(H, HKV, HD, pos + 500, n_tok, n_splits=3))]
+    assert ia.prefill_splits(calls[1][1]) > 1 and ia.decode_splits(calls[0][1]) > 1
+
+    def run(kind, desc, workspace):
+        print(f"[shared-ws] {kind} workspace={'shared' if workspace is ws else 'own'}", flush=True)
+        if kind == "decode":
+            out = torch.empty(H * HD, dtype=torch.float32, device=dev)
+            ia.attn_decode(qdec, kd, vd, out, desc, workspace=workspace)
+        else:
+            out = torch.empty(n_tok, H * HD, dtype=torch.float32, device=dev)
+            ia.attn_prefill(qpre, kd, vd, out, desc, workspace=workspace)
+        torch.cuda.synchronize()
+        return out.cpu().numpy().view(np.uint32)
+
+    want = [run(k, d, ia.Workspace(dev)) for k, d in calls]
+    for rep in range(2):
+        for i, (k, d) in enumerate(calls):
+            got = run(k, d, ws)
+            assert np.array_equal(got, want[i]), f"round {rep}, call {i} ({k}) differs on the shared workspace"
+            assert _counters_all_zero(ws), f"round {rep}, call {i} ({k}): counters not left at zero"
