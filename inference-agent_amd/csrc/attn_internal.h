@@ -62,7 +62,7 @@ int launch_prefill(const float* q, const _Float16* k, const _Float16* v, float* 
 // attn_any_slices(n_keys, 1) slices whose records (head_dim + 2 floats each, per head) go to
 // `part` and are merged by a second launch. Returns 0, -1 (grid too large), -2 (head_dim above
 // 1024) or -4 (launch failed).
-constexpr uint32_t kMinSliceKeys = 1024;
+constexpr uint32_t kMinSliceKeys = 256;
 constexpr uint32_t kMaxAnySlices = 64;
 uint32_t attn_any_slices(uint32_t n_keys, uint32_t n_tok);
 int launch_attn_any(const float* q, const _Float16* k, const _Float16* v, float* out, float* part, uint32_t pos,

@@ -107,8 +107,9 @@ def test_host_validation(lib):
                  ia.decode_desc(40, 8, 128, 4096), ia.decode_desc(32, 1, 128, 100),
                  ia.decode_desc(24, 8, 96, 4096), ia.decode_desc(4, 2, 1024, 9)):
         assert lib.ingot_attn_decode_workspace_size(ctypes.byref(good)) > 0
-    assert ia.decode_splits(ia.decode_desc(24, 8, 96, 4096)) == 4  # key slices of >= 1024
-    assert ia.decode_splits(ia.decode_desc(24, 8, 96, 1000)) == 1
+    assert ia.decode_splits(ia.decode_desc(24, 8, 96, 4096)) == 16  # key slices of >= 256
+    assert ia.decode_splits(ia.decode_desc(24, 8, 96, 1000)) == 4
+    assert ia.decode_splits(ia.decode_desc(24, 8, 96, 256)) == 1
     for bad in (ia.decode_desc(24, 8, 1025, 4096), # head_dim above 1024
                 ia.decode_desc(24, 7, 128, 4096),  # not divisible
                 ia.decode_desc(512, 8, 128, 4096), # more query heads than epoch words

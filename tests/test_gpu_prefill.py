@@ -224,7 +224,10 @@ def test_prefill_mfma_head_dims(dev, oracle_mod, hd, n_head, n_head_kv, pos, n_t
 
 @pytest.mark.parametrize("hd,n_head,n_head_kv,pos,n_tok", [
     (80, 32, 8, 0, 70), (96, 24, 8, 1000, 37), (112, 12, 4, 300, 5), (160, 8, 2, 0, 300),
-    (20, 4, 4, 17, 9), (1024, 2, 1, 260, 3), (3, 6, 3, 0, 40), (96, 8, 2, 3000, 1)])
+    (20, 4, 4, 17, 9), (1024, 2, 1, 260, 3), (3, 6, 3, 0, 40), (96, 8, 2, 3000, 1),
+    # blocks of 8 tokens (keys beyond one chunk): odd and 2-aligned rows, 1, 2 and 4 dim groups
+    # per thread
+    (3, 6, 3, 500, 20), (1023, 2, 1, 300, 9), (1022, 2, 1, 280, 10), (510, 4, 2, 700, 17)])
 def test_prefill_fallback_head_dims(dev, oracle_mod, hd, n_head, n_head_kv, pos, n_tok):
     # Head sizes without an MFMA kernel run the fallback kernel, the counterpart of the
     # reference's naive attention (shaders/kernels.metal:639-702, chosen at
