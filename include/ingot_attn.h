@@ -108,6 +108,14 @@ typedef struct IngotRopeKvDesc {
 size_t ingot_attn_decode_workspace_size(const IngotAttnDecodeDesc* d);
 size_t ingot_attn_prefill_workspace_size(const IngotAttnPrefillDesc* d);
 
+/* The most key splits a prefill call uses (n_splits = 0 chooses at most this many). The split
+ * count chosen for a chunk depends on its position, not monotonically, so the prefill workspace
+ * that serves every chunk of up to n_batch tokens in a context of n_ctx is
+ * ingot_attn_prefill_workspace_size() of the descriptor with pos = n_ctx - n_batch,
+ * n_tok = n_batch and n_splits = INGOT_ATTN_MAX_PREFILL_SPLITS. The decode workspace grows with
+ * n_keys: n_keys = n_ctx gives the largest. */
+#define INGOT_ATTN_MAX_PREFILL_SPLITS 16
+
 /* Split count the library would use for this descriptor (after n_splits = 0 resolution). */
 uint32_t ingot_attn_decode_splits(const IngotAttnDecodeDesc* d);
 uint32_t ingot_attn_prefill_splits(const IngotAttnPrefillDesc* d);

@@ -10,7 +10,7 @@ namespace ingot {
 
 // Upper bounds on split counts; they size the workspace.
 constexpr uint32_t kMaxDecodeSplits = 32;
-constexpr uint32_t kMaxPrefillSplits = 16;
+constexpr uint32_t kMaxPrefillSplits = 16;  // INGOT_ATTN_MAX_PREFILL_SPLITS (include/ingot_attn.h)
 // Decode hand-off counters (decode_merge.h): one per workgroup unit (at most one per query head),
 // each on its own 256-byte line (no false sharing of the device-scope atomics between units).
 constexpr uint32_t kCounterStride = 64;  // uint32 words

@@ -53,11 +53,14 @@ public:
             throw std::runtime_error("hip: rope_inv_freq must have head_dim/2 entries");
         kv_dim_ = size_t(c.n_head_kv) * c.head_dim;
         const size_t cache_bytes = size_t(c.n_layer) * c.n_ctx * kv_dim_ * 2;
-        // One workspace serves every call: the largest decode (n_keys = n_ctx) and the largest
-        // prefill chunk of each length at the end of the context.
+        // One workspace serves every call: the largest decode (n_keys = n_ctx) and the bound on
+        // every prefill chunk (the most splits of the longest chunk at the end of the context;
+        // the split count the library picks is not monotonic in the position).
         ws_bytes_ = ingot_attn_decode_workspace_size_checked(uint32_t(c.n_ctx));
-        for (int n = 2; n <= std::min(c.n_batch, c.n_ctx); n++)
-            ws_bytes_ = std::max(ws_bytes_, prefill_ws(uint32_t(c.n_ctx - n), uint32_t(n)));
+        const int nb = std::min(c.n_batch, c.n_ctx);
+        if (nb >= 2)
+            ws_bytes_ = std::max(ws_bytes_, prefill_ws(uint32_t(c.n_ctx - nb), uint32_t(nb),
+                                                       INGOT_ATTN_MAX_PREFILL_SPLITS));
         alloc(&kcache_, cache_bytes);
         alloc(&vcache_, cache_bytes);
         alloc(&ws_, ws_bytes_);
@@ -149,9 +152,9 @@ private:
         return n;
     }
 
-    size_t prefill_ws(uint32_t pos, uint32_t n_tok) const {
+    size_t prefill_ws(uint32_t pos, uint32_t n_tok, uint32_t n_splits) const {
         IngotAttnPrefillDesc d{uint32_t(c_.n_head), uint32_t(c_.n_head_kv), uint32_t(c_.head_dim),
-                               pos, n_tok, 0, uint32_t(c_.n_head * c_.head_dim), 0, 1.0f};
+                               pos, n_tok, 0, uint32_t(c_.n_head * c_.head_dim), n_splits, 1.0f};
         return ingot_attn_prefill_workspace_size(&d);
     }
 

@@ -264,3 +264,26 @@ def test_proj_rope_kv_checks(lib):
     assert call(q=None) == -1 and call(kc=None) == -1 and call(inv=None) == -1
     assert call(q=P((1 << 20) + 4)) == -1                                       # q alignment
     assert call(r=ia.rope_kv_desc(24, 8, 128, 5, 1, dst_offset=2)) == -1      # cache row alignment
+
+
+def test_prefill_workspace_bound_covers_every_chunk(lib):
+    """The prefill split count is not monotonic in the chunk's position (a 317-token chunk at
+    2867 needs more records than any chunk at the end of a 4096 context), so the workspace a
+    backend allocates once is the documented bound: the longest chunk at the end of the context
+    with INGOT_ATTN_MAX_PREFILL_SPLITS splits. Checked here against every chunk length and a
+    sweep of positions."""
+    import ingot_attn as ia
+
+    text = open(os.path.join(INCLUDE, "ingot_attn.h")).read()
+    max_splits = int(re.search(r"#define INGOT_ATTN_MAX_PREFILL_SPLITS (\d+)", text).group(1))
+
+    def size(nh, nkv, hd, pos, n, splits=0):
+        d = ia.prefill_desc(nh, nkv, hd, pos, n, n_splits=splits)
+        return lib.ingot_attn_prefill_workspace_size(ctypes.byref(d))
+
+    for nh, nkv, hd, n_ctx, n_batch in ((24, 8, 128, 4096, 512), (32, 8, 64, 2048, 256),
+                                        (16, 8, 256, 1500, 300), (32, 8, 128, 700, 512)):
+        bound = size(nh, nkv, hd, n_ctx - n_batch, n_batch, max_splits)
+        for n in range(2, n_batch + 1, 5):
+            for pos in range(0, n_ctx - n + 1, 37):
+                assert size(nh, nkv, hd, pos, n) <= bound, (nh, nkv, hd, n_ctx, n_batch, pos, n)
