@@ -39,7 +39,7 @@ def _case(dev, seed, n_head, n_head_kv, hd, L):
     return q, kb, vb, t(q), t(kb.view(np.int16)), t(vb.view(np.int16))
 
 
-@pytest.mark.parametrize("shape", [(24, 8, 128), (32, 8, 64), (16, 8, 256), (64, 8, 128)])
+@pytest.mark.parametrize("shape", [(24, 8, 128), (32, 8, 64), (16, 8, 256), (64, 8, 128), (24, 8, 96)])
 def test_noalloc_matches_workspace_entry_point(dev, oracle_mod, shape):
     import torch
     import ingot_attn as ia
