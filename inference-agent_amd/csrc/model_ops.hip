@@ -17,6 +17,12 @@ namespace {
 
 // One workgroup per row; 256 threads, float4 per thread per iteration. out may alias x (each
 // thread rewrites only the elements it read).
+// One workgroup per row. Thread t sums the squares of the float4s at 4t, 4t + 1024, ... in that
+// order, then the wave sums, then the four wave partials in fixed order (the fused projection
+// prologue in linear.hip repeats exactly this order). Rows of up to kRowRegs * 1024 elements
+// are held in registers with every load of x and w issued up front (a row of 3072: one round
+// trip instead of three dependent ones).
+constexpr int kRowRegs = 8;
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* __restrict__ w,
                                                       float* out, uint32_t n, float eps) {
     __shared__ float part[4];
@@ -24,9 +30,27 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
     const float* xr = x + size_t(row) * n;
     float* orow = out + size_t(row) * n;
     float ss = 0.f;
-    for (uint32_t i = 4 * tid; i < n; i += 1024) {
-        const float4v v = *reinterpret_cast<const float4v*>(xr + i);
-        ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+    const bool held = n <= 1024u * kRowRegs;
+    float4v xv[kRowRegs], wv[kRowRegs];
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kRowRegs; k++) {
+            const uint32_t i = 4 * tid + 1024 * k;
+            if (i < n) {
+                xv[k] = *reinterpret_cast<const float4v*>(xr + i);
+                wv[k] = *reinterpret_cast<const float4v*>(w + i);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kRowRegs; k++) {
+            const uint32_t i = 4 * tid + 1024 * k;
+            if (i < n) ss += xv[k][0] * xv[k][0] + xv[k][1] * xv[k][1] + xv[k][2] * xv[k][2] + xv[k][3] * xv[k][3];
+        }
+    } else {
+        for (uint32_t i = 4 * tid; i < n; i += 1024) {
+            const float4v v = *reinterpret_cast<const float4v*>(xr + i);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
     }
     ss = row16_sum(ss);
     ss += __shfl_xor(ss, 16);
@@ -35,10 +59,18 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const floa
     __syncthreads();
     const float total = (part[0] + part[1]) + (part[2] + part[3]);
     const float scale = 1.0f / sqrtf(total / float(n) + eps);
-    for (uint32_t i = 4 * tid; i < n; i += 1024) {
-        const float4v v = *reinterpret_cast<const float4v*>(xr + i);
-        const float4v g = *reinterpret_cast<const float4v*>(w + i);
-        *reinterpret_cast<float4v*>(orow + i) = v * scale * g;
+    if (held) {
+#pragma unroll
+        for (int k = 0; k < kRowRegs; k++) {
+            const uint32_t i = 4 * tid + 1024 * k;
+            if (i < n) *reinterpret_cast<float4v*>(orow + i) = xv[k] * scale * wv[k];
+        }
+    } else {
+        for (uint32_t i = 4 * tid; i < n; i += 1024) {
+            const float4v v = *reinterpret_cast<const float4v*>(xr + i);
+            const float4v g = *reinterpret_cast<const float4v*>(w + i);
+            *reinterpret_cast<float4v*>(orow + i) = v * scale * g;
+        }
     }
 }
 

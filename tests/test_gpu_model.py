@@ -55,7 +55,7 @@ def test_rmsnorm(dev, oracle_mod):
     import ingot_attn as ia
 
     rng = np.random.default_rng(1)
-    for n, rows in ((3072, 1), (3072, 37), (512, 4), (8192, 2)):
+    for n, rows in ((3072, 1), (3072, 37), (512, 4), (100, 5), (12288, 3), (8192, 2)):
         x = rng.standard_normal((rows, n)).astype(np.float32) * 3
         w = rng.standard_normal(n).astype(np.float32)
         out = torch.empty(rows, n, dtype=torch.float32, device=dev)
