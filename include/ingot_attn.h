@@ -30,7 +30,8 @@
  * decode and prefill, as the reference serves them (its flash kernels cover head_dim 128 —
  * decode with groups up to 4, src/metal_backend.mm:339, prefill any group, :360 — and its naive
  * kernel every other shape, src/metal_backend.mm:373-382, shaders/kernels.metal:639-702, with
- * one thread per head dimension, so up to 1024). Here head_dim 128 decode with groups 1..4 runs
+ * one thread per head dimension, so up to 1024). Here head_dim 128 decode with groups 1..4 (and
+ * groups that are multiples of 3 or 4, as units of 3 or 4 heads) runs
  * the tuned kernel (attn_decode.hip), other head_dim 64/256/128 decode shapes the generic split
  * kernel, prefill at 64/128/256 the MFMA kernel (units of up to 3 heads, 1 at head_dim 256), and
  * every other head_dim the fallback kernel (attn_naive.hip, never split). At most 256 query

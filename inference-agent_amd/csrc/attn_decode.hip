@@ -1,5 +1,8 @@
 // attn_decode.hip — split-KV (flash-decoding) GQA decode attention for gfx950: the tuned kernel
-// for head_dim 128 and groups 1..4 (Llama-3.2-3B: group 3); attn_decode_any.hip serves the other
+// for head_dim 128 and groups 1..4 (Llama-3.2-3B: group 3), and for larger groups that are
+// multiples of 3 or 4 as n_sub units of 3 or 4 heads per KV head (group 8: 64/8 heads, KV 1024
+// 8.50 -> 7.08 us, 4096 10.40 -> 10.11; each unit streams the KV head's slice, the second read
+// served by the caches); attn_decode_any.hip serves the other
 // shapes.
 //
 // Computes, for one query token and every Q head h, out_h = softmax(q_h K^T * scale) V over cache
@@ -7,10 +10,10 @@
 // decode flash path of src/metal_backend.mm:339-359 (attn_decode_g3 + attn_combine,
 // shaders/kernels.metal:428-516), re-designed for CDNA4.
 //
-// Grid: one dimension of n_splits * n_head_kv workgroups, workgroup b serving KV head
-// b % n_head_kv and key slice b / n_head_kv. The hardware hands workgroups to the 8 XCDs round
-// robin (b % 8), so with 8 KV heads every slice of one KV head runs on the same XCD and its
-// records meet in one L2. Each workgroup has NW wave64s; a wave step covers 16 keys and serves all
+// Grid: one dimension of n_splits * n_units workgroups (n_units = n_head_kv * n_sub), workgroup
+// b serving unit b % n_units (query heads unit*G.., KV head unit / n_sub) and key slice
+// b / n_units. The hardware hands workgroups to the 8 XCDs round robin (b % 8), so with 8 KV
+// heads and one unit each every slice of one KV head runs on the same XCD. Each workgroup has NW wave64s; a wave step covers 16 keys and serves all
 // G query heads of the group from each K/V row it reads:
 //   - Scores on the matrix cores: S (16 rows x 16 keys) = A (16 x 256) * B (256 x 16) with
 //     v_mfma_f32_16x16x32_f16 x 8. Rows 0..G-1 of A hold the G query heads; the 256-long
@@ -42,6 +45,8 @@
 // Record layout (workspace, after the counters): one region of kDecodeHeadRecordBytes per query
 // head, [split][528 bytes]: o[128] (unnormalized, relative to m), then m (base 2) and l — the
 // reference's part[...][130] record (AD_STRIDE, shaders/kernels.metal:291).
+#include <type_traits>
+
 #include "attn_common.h"
 #include "attn_internal.h"
 #include "decode_merge.h"
@@ -58,11 +63,11 @@ __device__ __forceinline__ float lane0(float x) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
 }
 
-template <int G, int NW, bool ROT>
+template <int G, int NW, bool ROT, bool SUB>
 __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     const float* __restrict__ q, const _Float16* __restrict__ K, const _Float16* __restrict__ V,
     float* __restrict__ out, char* __restrict__ recs, unsigned int* __restrict__ counters,
-    uint32_t n_keys, uint32_t keys_per_split, uint32_t n_splits, uint32_t n_head_kv,
+    uint32_t n_keys, uint32_t keys_per_split, uint32_t n_splits, uint32_t n_units, uint32_t n_sub,
     float qscale) {
     static_assert(G <= NW, "one tail wave per query head of the group");
     static_assert(kMaxDecodeSplits <= 64, "one lane per split in the merge");
@@ -75,8 +80,10 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r = lane >> 4, c = lane & 15;
-    const uint32_t kvh = blockIdx.x % n_head_kv, split = blockIdx.x / n_head_kv;
-    const size_t kv_dim = size_t(n_head_kv) * kHeadDim;
+    // unit = query heads unit*G .. unit*G+G-1 of KV head unit / n_sub (n_sub units share a KV
+    // head when the group is larger than G)
+    const uint32_t unit = blockIdx.x % n_units, split = blockIdx.x / n_units, kvh = SUB ? unit / n_sub : unit;
+    const size_t kv_dim = size_t(n_units / n_sub) * kHeadDim;
     const uint32_t k0 = split * keys_per_split;
     const uint32_t k1 = min(n_keys, k0 + keys_per_split);
 
@@ -102,7 +109,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
     half8 qa[8];
     {
         const bool live = c < G;
-        const float* qrow = q + (size_t(kvh) * G + (live ? c : 0)) * kHeadDim;
+        const float* qrow = q + (size_t(unit) * G + (live ? c : 0)) * kHeadDim;
 #pragma unroll
         for (int m = 0; m < 4; m++) {
             const float4v* src = reinterpret_cast<const float4v*>(qrow + 32 * m + 8 * r);
@@ -240,7 +247,7 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
         for (int g = 1; g < 4; g++) s4 += *reinterpret_cast<const float4v*>(&lds_o[w][g][h][4 * j]);
         O += s4 * wt;
     }
-    const size_t head = size_t(kvh) * G + h;
+    const size_t head = size_t(unit) * G + h;
     if (n_splits == 1) {
         if (lane < 32) handoff::store_out(out + head * kHeadDim, kHeadDim * 4, 16 * j, O * (L > 0.f ? 1.f / L : 0.f));
         return;
@@ -258,13 +265,26 @@ __global__ __launch_bounds__(64 * NW) void attn_decode_kernel(
 template <int G, int NW>
 void launch_g(uint32_t n_blocks, hipStream_t stream, const float* q, const _Float16* k,
               const _Float16* v, float* out, char* recs, unsigned int* counters, uint32_t n_keys,
-              uint32_t per, uint32_t n_splits, uint32_t n_head_kv, float qscale) {
-    if (n_splits > 1 && (per + 16 * NW - 1) / (16 * NW) >= 3)  // several slices of 3+ steps
-        hipLaunchKernelGGL((attn_decode_kernel<G, NW, true>), dim3(n_blocks), dim3(64 * NW), 0, stream, q,
-                           k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale);
-    else
-        hipLaunchKernelGGL((attn_decode_kernel<G, NW, false>), dim3(n_blocks), dim3(64 * NW), 0, stream, q,
-                           k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale);
+              uint32_t per, uint32_t n_splits, uint32_t n_units, uint32_t n_sub, float qscale) {
+    // (SUB: several units per KV head, which costs the one-split-per-head case an integer
+    // division before its first loads; instantiated for the unit sizes that large groups use)
+    auto go = [&](auto rot, auto sub) {
+        hipLaunchKernelGGL((attn_decode_kernel<G, NW, decltype(rot)::value, decltype(sub)::value>), dim3(n_blocks),
+                           dim3(64 * NW), 0, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_units,
+                           n_sub, qscale);
+    };
+    const bool rot = n_splits > 1 && (per + 16 * NW - 1) / (16 * NW) >= 3;  // several slices of 3+ steps
+    using T = std::true_type;
+    using F = std::false_type;
+    if constexpr (G >= 3) {
+        if (n_sub > 1) {
+            if (rot) go(T{}, T{});
+            else go(F{}, T{});
+            return;
+        }
+    }
+    if (rot) go(T{}, F{});
+    else go(F{}, F{});
 }
 
 constexpr int kNW = 4;
@@ -275,13 +295,22 @@ int launch_decode_g128(const float* q, const _Float16* k, const _Float16* v, flo
                        unsigned int* counters, uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv,
                        uint32_t group, float scale, hipStream_t stream) {
     const uint32_t per = (n_keys + n_splits - 1) / n_splits;
-    const uint32_t blocks = n_splits * n_head_kv;
+    // Groups above 4 run as units of gs heads (the largest divisor of the group up to 4), n_sub
+    // units per KV head, each streaming that KV head's slice.
+    uint32_t gs = group;
+    if (group > 4) {
+        gs = 1;
+        for (uint32_t g = 4; g > 1; g--)
+            if (group % g == 0) { gs = g; break; }
+    }
+    const uint32_t n_sub = group / gs, n_units = n_head_kv * n_sub;
+    const uint32_t blocks = n_splits * n_units;
     const float qscale = scale * kLog2e;
-    switch (group) {
-        case 1: launch_g<1, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 2: launch_g<2, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 3: launch_g<3, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
-        case 4: launch_g<4, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_head_kv, qscale); break;
+    switch (gs) {
+        case 1: launch_g<1, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_units, n_sub, qscale); break;
+        case 2: launch_g<2, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_units, n_sub, qscale); break;
+        case 3: launch_g<3, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_units, n_sub, qscale); break;
+        case 4: launch_g<4, kNW>(blocks, stream, q, k, v, out, recs, counters, n_keys, per, n_splits, n_units, n_sub, qscale); break;
         default: return -2;
     }
     return hipGetLastError() == hipSuccess ? 0 : -4;

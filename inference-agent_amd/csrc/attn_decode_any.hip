@@ -1,5 +1,6 @@
 // attn_decode_any.hip — split-KV GQA decode attention for any head_dim in {64, 128, 256} and any
-// group size (gfx950); attn_decode.hip holds the tuned kernel for head_dim 128 and groups 1..4.
+// group size (gfx950); attn_decode.hip holds the tuned kernel for head_dim 128 and groups 1..4
+// (and multiples of 3 or 4).
 //
 // Computes, for one query token and every Q head h, out_h = softmax(q_h K^T * scale) V over cache
 // rows 0..n_keys-1 of KV head h / group — the attention block of src/cpu_backend.cpp:51-69 and
@@ -373,7 +374,7 @@ int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* o
                   uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
                   uint32_t head_dim, float scale, hipStream_t stream) {
     char* ws = static_cast<char*>(workspace);
-    if (head_dim == 128 && group <= 4)
+    if (head_dim == 128 && (group <= 4 || group % 4 == 0 || group % 3 == 0))
         return launch_decode_g128(q, k, v, out, ws + kCounterBytes,
                                   reinterpret_cast<unsigned int*>(ws), n_keys, n_splits, n_head_kv, group,
                                   scale, stream);

@@ -38,9 +38,11 @@ uint32_t prefill_splits(uint32_t pos, uint32_t n_tok, uint32_t n_units, uint32_t
 uint32_t prefill_unit_heads(uint32_t group, uint32_t head_dim);
 constexpr size_t prefill_record_bytes(uint32_t head_dim) { return head_dim * 2 + 16; }
 
-// Decode attention, dispatched by launch_decode: head_dim 128 with groups 1..4 take the tuned
-// kernel (attn_decode.hip), every other shape the generic one (attn_decode_any.hip). Both keep
-// their hand-off counters in the workspace's first kCounterBytes and the records after them. Return 0, -1 (grid too large), -2 (shape without a kernel) or -4 (launch failed).
+// Decode attention, dispatched by launch_decode: head_dim 128 with groups 1..4 (or multiples of
+// 3 or 4) take the tuned kernel (attn_decode.hip), every other shape the generic one
+// (attn_decode_any.hip). Both keep their hand-off counters in the workspace's first
+// kCounterBytes and the records after them. Return 0, -1 (grid too large), -2 (shape without a
+// kernel) or -4 (launch failed).
 int launch_decode(const float* q, const _Float16* k, const _Float16* v, float* out, void* workspace,
                   uint32_t n_keys, uint32_t n_splits, uint32_t n_head_kv, uint32_t group,
                   uint32_t head_dim, float scale, hipStream_t stream);
