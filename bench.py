@@ -40,9 +40,9 @@ sys.path.insert(0, os.path.join(ROOT, "inference-agent_amd"))
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E, 8 TB/s
 # HBM bytes per C3 decode launch: (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0) KiB from rocprofv3, the
 # factors from the copy probe (profiles/attn_decode_C3_traffic.md).
-C3_TRAFFIC_BYTES = int((8465.0 * 2.0 + 444.75) * 1024)
+C3_TRAFFIC_BYTES = int((8461.0 * 2.0 + 444.75) * 1024)
 C3_TRAFFIC_SOURCE = ("profiles/attn_decode_C3_traffic.md: rocprofv3 FETCH_SIZE x2.0 + WRITE_SIZE x1.0 "
-                     "of attn_decode_kernel<3,4,false> (inference-agent_amd/csrc/attn_decode.hip)")
+                     "of attn_decode_kernel<3,4,false,false> (inference-agent_amd/csrc/attn_decode.hip)")
 MFMA_F16_PEAK_TFS = 2500.0  # MI355X dense f16 MFMA, 2.5 PFLOP/s
 WARMUP_SECONDS = 0.3
 METRIC = "decode-attn HBM GB/s + prefill-attn TFLOPS, Llama-3.2-3B GQA, 1 MI355X"
@@ -519,7 +519,7 @@ def main():
         roofline = {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                     "traffic": C3_TRAFFIC_BYTES, "traffic_source": C3_TRAFFIC_SOURCE,
-                    "kernel": "attn_decode_kernel<3,4,false>",
+                    "kernel": "attn_decode_kernel<3,4,false,false>",
                     "bytes_per_launch": nbytes, "us_per_launch": round(us_thru, 3)}
         workload = ("C3 decode attention, KV 4096, 24 Q / 8 KV heads, hd 128, f16 cache, "
                     "28-layer slice rotation (470 MB)")
