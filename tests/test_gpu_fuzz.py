@@ -1,7 +1,7 @@
 """Seeded random sweeps of decode and prefill shapes through the C ABI against the CPU oracle:
 head size (the MFMA sizes 64/128/256 and odd sizes for the fallback kernel), group size, cache
 length, chunk position and length, forced or library-chosen splits, a layer offset into a
-multi-layer cache and a padded q_stride — combinations the hand-picked cases do not reach.
+multi-layer cache, a padded q_stride and the descriptor's scale — combinations the hand-picked cases do not reach.
 Every case prints its parameters before the GPU call. Bar: max|d| <= 2e-3, rel-L2 <= 1e-3."""
 from __future__ import annotations
 
@@ -57,16 +57,17 @@ def test_decode_random_shapes(dev, oracle_mod, case):
     n_layer, layer = 3, int(rng.integers(3))
     n_ctx = L + int(rng.integers(0, 40))
     kv_dim = n_head_kv * hd
+    scale = None if case % 3 else float(rng.choice([0.02, 0.3, 1.0]))  # the descriptor's own scale
     print(f"[fuzz decode {case}] {n_head}/{n_head_kv} hd={hd} L={L} splits={splits} layer={layer} "
-          f"n_ctx={n_ctx}", flush=True)
+          f"n_ctx={n_ctx} scale={scale}", flush=True)
     kb, vb = _cache(rng, n_layer, n_ctx, kv_dim, L, layer)
     q = rng.standard_normal(n_head * hd).astype(np.float32)
     out = torch.full((n_head * hd,), float("nan"), dtype=torch.float32, device=dev)
-    desc = ia.decode_desc(n_head, n_head_kv, hd, L, kv_offset=layer * n_ctx * kv_dim, n_splits=splits)
+    desc = ia.decode_desc(n_head, n_head_kv, hd, L, kv_offset=layer * n_ctx * kv_dim, n_splits=splits, scale=scale)
     ia.attn_decode(_t(q, dev), _t(kb.view(np.int16), dev), _t(vb.view(np.int16), dev), out, desc)
     torch.cuda.synchronize()
     r0 = layer * n_ctx
-    want = oracle_mod.attn_decode(q, kb[r0:r0 + L], vb[r0:r0 + L], n_head, n_head_kv, hd, L, threads=8)
+    want = oracle_mod.attn_decode(q, kb[r0:r0 + L], vb[r0:r0 + L], n_head, n_head_kv, hd, L, scale=scale, threads=8)
     assert_parity(out.cpu().numpy(), want, f"decode case {case}")
 
 
@@ -87,20 +88,23 @@ def test_prefill_random_shapes(dev, oracle_mod, case):
     kv_dim = n_head_kv * hd
     pad = int(rng.choice([0, 0, 4, 36]))  # q_stride padding (a multiple of 4)
     q_stride = n_head * hd + pad
+    # (the MFMA prefill rounds q * scale to f16, as the reference's GPU path does, so the score
+    # error grows with the scale: scales of the size attention uses, around 1/sqrt(head_dim))
+    scale = None if case % 3 else float(rng.choice([0.02, 0.06, 0.12]))
     print(f"[fuzz prefill {case}] {n_head}/{n_head_kv} hd={hd} pos={pos} n_tok={n_tok} splits={splits} "
-          f"layer={layer} q_stride={q_stride}", flush=True)
+          f"layer={layer} q_stride={q_stride} scale={scale}", flush=True)
     kb, vb = _cache(rng, n_layer, n_ctx, kv_dim, L, layer)
     qf = np.full((n_tok, q_stride), np.nan, dtype=np.float32)
     qf[:, :n_head * hd] = rng.standard_normal((n_tok, n_head * hd)).astype(np.float32)
     out = torch.full((n_tok, q_stride), float("nan"), dtype=torch.float32, device=dev)
     desc = ia.prefill_desc(n_head, n_head_kv, hd, pos, n_tok, kv_offset=layer * n_ctx * kv_dim,
-                           q_stride=q_stride, n_splits=splits)
+                           q_stride=q_stride, n_splits=splits, scale=scale)
     ia.attn_prefill(_t(qf, dev), _t(kb.view(np.int16), dev), _t(vb.view(np.int16), dev), out, desc)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     r0 = layer * n_ctx
     want = oracle_mod.attn_prefill(qf[:, :n_head * hd], kb[r0:r0 + L], vb[r0:r0 + L], n_head, n_head_kv, hd,
-                                   pos, n_tok, threads=8)
+                                   pos, n_tok, scale=scale, threads=8)
     assert_parity(got[:, :n_head * hd], want.reshape(n_tok, -1), f"prefill case {case}")
     if pad:
         assert np.isnan(got[:, n_head * hd:]).all(), "the padding columns of out were written"
