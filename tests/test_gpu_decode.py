@@ -136,10 +136,13 @@ def test_decode_head_dims(dev, oracle_mod, n_head, n_head_kv, hd, L):
 
 
 @pytest.mark.parametrize("n_head,n_head_kv,hd", [(64, 8, 128), (40, 8, 128), (32, 1, 128), (12, 2, 64),
-                                                  (10, 2, 256), (56, 8, 64), (14, 2, 128)])
+                                                  (10, 2, 256), (56, 8, 64), (14, 2, 128), (48, 8, 128),
+                                                  (96, 8, 128), (18, 1, 128)])
 def test_decode_large_groups(dev, oracle_mod, n_head, n_head_kv, hd):
-    # Groups above 4 (the reference's flash decode limit, src/metal_backend.mm:339): up to 8
-    # heads share one workgroup, larger groups take several workgroups per KV head.
+    # Groups above 4 (the reference's flash decode limit, src/metal_backend.mm:339): at head_dim
+    # 128 groups that are multiples of 4 or 3 run the tuned kernel as units of 4 or 3 heads per
+    # KV head (64/8, 96/8, 32/1: units of 4; 48/8, 18/1: units of 3); other groups and head
+    # sizes the generic kernel, up to 8 heads per workgroup, larger groups over several.
     L = 1500
     q, kb, vb = _inputs(7 * n_head + hd, n_head, n_head_kv, L, hd=hd)
     got = _run_decode(dev, q, kb, vb, n_head, n_head_kv, L, hd=hd)

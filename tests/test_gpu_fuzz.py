@@ -13,7 +13,7 @@ from conftest import assert_parity, ensure_built
 pytestmark = pytest.mark.gpu
 
 HEAD_DIMS = [64, 128, 128, 128, 256, 96, 80, 40, 18]
-GROUPS = [(8, 8), (16, 8), (24, 8), (32, 8), (12, 4), (40, 8), (64, 8), (6, 2), (4, 1)]
+GROUPS = [(8, 8), (16, 8), (24, 8), (32, 8), (12, 4), (40, 8), (64, 8), (6, 2), (4, 1), (48, 8), (96, 8)]
 
 
 @pytest.fixture(scope="module")
